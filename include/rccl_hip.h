@@ -1,0 +1,233 @@
+/*
+ * rccl_hip: MI355X (gfx950) ordering primitives behind a plain C ABI.
+ *
+ * This is the drop-in boundary for the ordering hot path of StarGazerM/rccl
+ * (a Rust CUB/Thrust reimplementation). Each entry point replaces one family
+ * of the reference's public functions; the comment above it cites the
+ * reference interface (paths relative to that tree). A Rust binding would
+ * declare these in an `extern "C"` block and keep the reference's public
+ * surface (Program, Launch/Execution, views, typed workspaces) on top.
+ *
+ * Conventions (rccl-cub/src/error.rs:3-25, SURVEY of rccl-thrust/src/cuda.rs):
+ *  - All pointers are device pointers unless stated otherwise; sizes are in
+ *    elements. The caller owns inputs, outputs and the workspace; no entry
+ *    point allocates device memory.
+ *  - Work is enqueued on `stream` and is asynchronous (CUB semantics). The
+ *    Thrust-style synchronous behaviour is the host layer's job.
+ *  - Every call validates all arguments before the first launch and returns a
+ *    status that maps 1:1 onto DeviceAlgorithmError. Details of the last
+ *    failure on the calling thread are available from rccl_hip_last_error().
+ *  - Empty inputs (and empty radix bit windows) return success without
+ *    launching anything.
+ */
+#ifndef RCCL_HIP_H
+#define RCCL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RCCL_HIP_ABI_VERSION 1
+
+#if defined(__GNUC__) || defined(__clang__)
+#define RCCL_HIP_API __attribute__((visibility("default")))
+#else
+#define RCCL_HIP_API
+#endif
+
+/* Status codes: DeviceAlgorithmError variants (rccl-cub/src/error.rs:3-17). */
+typedef enum rccl_hip_status {
+  RCCL_HIP_SUCCESS = 0,
+  RCCL_HIP_ERROR_LENGTH_MISMATCH = 1,     /* LengthMismatch{role,expected,actual} */
+  RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL = 2, /* WorkspaceTooSmall{role,required,actual} */
+  RCCL_HIP_ERROR_INVALID_BIT_RANGE = 3,   /* InvalidBitRange{begin,end,key_bits} */
+  RCCL_HIP_ERROR_UNSUPPORTED_TARGET = 4,  /* UnsupportedTarget(msg) */
+  RCCL_HIP_ERROR_SIZE_OVERFLOW = 5,       /* SizeOverflow */
+  RCCL_HIP_ERROR_MEMORY = 6,              /* Memory(MemoryError) */
+  RCCL_HIP_ERROR_DRIVER = 7,              /* Driver(DriverError): a HIP call failed */
+  RCCL_HIP_ERROR_LAUNCH = 8,              /* Launch(LaunchContractError) */
+  RCCL_HIP_ERROR_INVALID_ARGUMENT = 9     /* a null pointer or unknown enum value */
+} rccl_hip_status;
+
+/* Key types. 0..5 are the radix-sortable RadixKey set
+ * (rccl-cub/src/radix.rs:114-173); merge, merge sort and set operations also
+ * accept the 8/16-bit integers, which the reference reaches through generic
+ * DeviceCopy keys with a natural-order closure. */
+typedef enum rccl_hip_key_kind {
+  RCCL_HIP_KEY_U32 = 0,
+  RCCL_HIP_KEY_I32 = 1,
+  RCCL_HIP_KEY_F32 = 2,
+  RCCL_HIP_KEY_U64 = 3,
+  RCCL_HIP_KEY_I64 = 4,
+  RCCL_HIP_KEY_F64 = 5,
+  RCCL_HIP_KEY_U8 = 6,
+  RCCL_HIP_KEY_I8 = 7,
+  RCCL_HIP_KEY_U16 = 8,
+  RCCL_HIP_KEY_I16 = 9
+} rccl_hip_key_kind;
+
+/* Comparator variants. A reference closure `|a, b| a.cmp(b)` (or the
+ * closure-free natural order, rccl-thrust/src/merge.rs:169-178) lowers to
+ * ASCENDING and `|a, b| b.cmp(a)` to DESCENDING. For floats the order is IEEE
+ * `<` (-0.0 and +0.0 are equivalent). */
+typedef enum rccl_hip_order {
+  RCCL_HIP_ORDER_ASCENDING = 0,
+  RCCL_HIP_ORDER_DESCENDING = 1
+} rccl_hip_order;
+
+/* Set operations (rccl-cub/src/ordering_backend/set.rs:564-827). */
+typedef enum rccl_hip_set_operation {
+  RCCL_HIP_SET_UNION = 0,
+  RCCL_HIP_SET_INTERSECTION = 1,
+  RCCL_HIP_SET_DIFFERENCE = 2,
+  RCCL_HIP_SET_SYMMETRIC_DIFFERENCE = 3
+} rccl_hip_set_operation;
+
+/* Details of the most recent failing call on this thread. `role` names the
+ * offending range, as the reference's `role: &'static str` does. */
+typedef struct rccl_hip_error_info {
+  rccl_hip_status status;
+  const char *role;     /* static string; never NULL */
+  uint64_t expected;    /* LengthMismatch.expected / WorkspaceTooSmall.required */
+  uint64_t actual;
+  uint32_t begin_bit;   /* InvalidBitRange */
+  uint32_t end_bit;
+  uint32_t key_bits;
+  int hip_error;        /* hipError_t for DRIVER/LAUNCH, else 0 */
+} rccl_hip_error_info;
+
+/* Copy the last error of the calling thread into *info. */
+RCCL_HIP_API void rccl_hip_last_error(rccl_hip_error_info *info);
+/* Static description of a status code. */
+RCCL_HIP_API const char *rccl_hip_status_string(rccl_hip_status status);
+/* RCCL_HIP_ABI_VERSION of the loaded library. */
+RCCL_HIP_API int rccl_hip_abi_version(void);
+
+/* Check that `device` is a gfx950 GPU the kernels were built for. Replaces
+ * Program::load (rccl-cub/src/cuda.rs:749-756, rccl-thrust/src/cuda.rs:85-91)
+ * and the target gate ensure_radix_target (rccl-cub/src/radix.rs:14-22).
+ * Returns UNSUPPORTED_TARGET on any other architecture. */
+RCCL_HIP_API rccl_hip_status rccl_hip_program_load(int device);
+
+/* ------------------------------------------------------------------------
+ * DeviceRadixSort
+ * ------------------------------------------------------------------------ */
+
+/* Bytes of control workspace (bins, look-back descriptors, tile counters) a
+ * radix sort of n items needs. value_bytes is 0 for keys-only, else one of
+ * 1, 2, 4, 8, 16. Replaces device_radix_sort_{keys,pairs}_buffer_workspace
+ * and the control part of device_radix_sort_{,pairs_}workspace
+ * (rccl-cub/src/workspace.rs:108-177). The workspace needs no initialisation
+ * and may be reused by later calls on the same stream. */
+RCCL_HIP_API rccl_hip_status rccl_hip_radix_sort_workspace_bytes(rccl_hip_key_kind key,
+                                                    size_t value_bytes, size_t n,
+                                                    size_t *bytes);
+
+/* Double-buffer radix sort over bits [begin_bit, end_bit) of the key's
+ * order-preserving bit image. Input is the buffer selected by
+ * *current_is_first (1: keys_first/values_first); the result lands in the
+ * buffer *current_is_first selects on return, the other buffer is clobbered.
+ * values_first/values_second are NULL iff value_bytes == 0.
+ * Replaces device_radix_sort_{keys,pairs}_buffer{,_descending}
+ * (rccl-cub/src/dispatch.rs:2091-2943; pass control rccl-cub/src/radix.rs:427-554,
+ * :627-759; DoubleBuffer rccl-cub/src/double_buffer.rs:6-130). Stable; no
+ * length cap below 2^32 items. */
+RCCL_HIP_API rccl_hip_status rccl_hip_radix_sort_buffer(rccl_hip_key_kind key, size_t value_bytes,
+                                           rccl_hip_order order, void *keys_first,
+                                           void *keys_second, void *values_first,
+                                           void *values_second, size_t n,
+                                           int *current_is_first, uint32_t begin_bit,
+                                           uint32_t end_bit, void *workspace,
+                                           size_t workspace_bytes, hipStream_t stream);
+
+/* In-place radix sort of all key bits with caller-owned scratch of n keys
+ * (and n values). Replaces device_radix_sort_{keys,pairs}{,_descending}
+ * (rccl-cub/src/radix.rs:558-623, :763-876): the result is copied back when
+ * it lands in the scratch buffer. */
+RCCL_HIP_API rccl_hip_status rccl_hip_radix_sort(rccl_hip_key_kind key, size_t value_bytes,
+                                    rccl_hip_order order, void *keys, void *values,
+                                    void *scratch_keys, void *scratch_values, size_t n,
+                                    void *workspace, size_t workspace_bytes,
+                                    hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * DeviceMerge
+ * ------------------------------------------------------------------------ */
+
+/* Workspace bytes for merging na + nb items. Replaces
+ * device_merge_{keys,pairs}_workspace (rccl-cub/src/workspace.rs:215-243). */
+RCCL_HIP_API rccl_hip_status rccl_hip_merge_workspace_bytes(rccl_hip_key_kind key, size_t value_bytes,
+                                               size_t na, size_t nb, size_t *bytes);
+
+/* Stable merge of two sorted ranges into out (na + nb items); on equivalent
+ * keys every item of A precedes those of B. Values (value_bytes > 0) follow
+ * their keys. Replaces device_merge_keys/device_merge_pairs
+ * (rccl-cub/src/dispatch.rs:1572,1915; rccl-cub/src/merge.rs:194-368) and the
+ * Thrust merge(..).write_into forms (rccl-thrust/src/merge.rs:83-247). */
+RCCL_HIP_API rccl_hip_status rccl_hip_merge(rccl_hip_key_kind key, size_t value_bytes,
+                               rccl_hip_order order, const void *a_keys,
+                               const void *a_values, size_t na, const void *b_keys,
+                               const void *b_values, size_t nb, void *out_keys,
+                               void *out_values, void *workspace, size_t workspace_bytes,
+                               hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * DeviceMergeSort
+ * ------------------------------------------------------------------------ */
+
+/* Workspace bytes (scratch keys/values and partitions) for a merge sort of n
+ * items. Replaces device_merge_sort_{keys,pairs}_workspace
+ * (rccl-cub/src/workspace.rs:251-285). */
+RCCL_HIP_API rccl_hip_status rccl_hip_merge_sort_workspace_bytes(rccl_hip_key_kind key,
+                                                    size_t value_bytes, size_t n,
+                                                    size_t *bytes);
+
+/* Stable merge sort. in_keys == out_keys (and in_values == out_values) sorts
+ * in place; otherwise the inputs are left untouched (the _copy forms).
+ * Replaces device_merge_sort_{keys,pairs}{,_copy}
+ * (rccl-cub/src/dispatch.rs:170-322,1116-1400; rccl-cub/src/merge_sort.rs:156-690)
+ * and Thrust sort_by / sort_unstable_by (rccl-thrust/src/backend.rs:39-150). */
+RCCL_HIP_API rccl_hip_status rccl_hip_merge_sort(rccl_hip_key_kind key, size_t value_bytes,
+                                    rccl_hip_order order, const void *in_keys,
+                                    const void *in_values, void *out_keys,
+                                    void *out_values, size_t n, void *workspace,
+                                    size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Set operations
+ * ------------------------------------------------------------------------ */
+
+/* Workspace bytes for a set operation over na + nb items. Replaces
+ * set_workspace_counts and the TemporaryWorkspace5 layout of
+ * rccl-thrust/src/set.rs:27-125 (rccl-cub/src/workspace.rs:287-357). */
+RCCL_HIP_API rccl_hip_status rccl_hip_set_op_workspace_bytes(rccl_hip_set_operation op, rccl_hip_key_kind key,
+                                                size_t value_bytes, size_t na, size_t nb,
+                                                size_t *bytes);
+
+/* Sorted multiset operation. Writes the result length to *d_out_count
+ * (device memory, one uint64_t). out_keys == NULL counts without writing
+ * keys (the `.count()` form); out_values is NULL iff value_bytes == 0 or
+ * out_keys == NULL. For INTERSECTION b_values is not read. The output buffers
+ * must hold the operation's maximum output (union/symmetric difference:
+ * na + nb; intersection: min(na, nb); difference: na).
+ * Replaces Launch::set_keys / set_pairs (rccl-cub/src/dispatch.rs:413-550;
+ * rccl-cub/src/set_operation.rs:265-589) and the Thrust union/intersection/
+ * difference/symmetric_difference expressions (rccl-thrust/src/set.rs:357-898). */
+RCCL_HIP_API rccl_hip_status rccl_hip_set_op(rccl_hip_set_operation op, rccl_hip_key_kind key,
+                                size_t value_bytes, rccl_hip_order order,
+                                const void *a_keys, const void *a_values, size_t na,
+                                const void *b_keys, const void *b_values, size_t nb,
+                                void *out_keys, void *out_values, uint64_t *d_out_count,
+                                void *workspace, size_t workspace_bytes,
+                                hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RCCL_HIP_H */

@@ -1,0 +1,158 @@
+"""Python access to the CPU oracle (oracle/oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py`` as the checker. The product
+(``rccl_amd``) never imports it.
+
+Every function mirrors one C function in ``oracle.c``; see that file for the
+reference file:line each one restates. Arrays are numpy arrays; sorting
+functions work on copies and return them.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+# Key kinds (numbering equals include/rccl_hip.h).
+KEY_KINDS = {
+    "u32": 0, "i32": 1, "f32": 2, "u64": 3, "i64": 4, "f64": 5,
+    "u8": 6, "i8": 7, "u16": 8, "i16": 9,
+}
+KIND_DTYPES = {
+    "u32": np.uint32, "i32": np.int32, "f32": np.float32,
+    "u64": np.uint64, "i64": np.int64, "f64": np.float64,
+    "u8": np.uint8, "i8": np.int8, "u16": np.uint16, "i16": np.int16,
+}
+SET_OPS = {"union": 0, "intersection": 1, "difference": 2, "symmetric_difference": 3}
+
+_lib = None
+
+
+def build() -> str:
+    """Compile liboracle.so with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], check=True)
+    return _LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        lib = ctypes.CDLL(_LIB_PATH)
+        c = ctypes
+        lib.oracle_splitmix64.restype = c.c_uint64
+        lib.oracle_splitmix64.argtypes = [c.c_uint64]
+        lib.oracle_radix_ordered.restype = c.c_uint64
+        lib.oracle_radix_ordered.argtypes = [c.c_int, c.c_int, c.c_uint64]
+        lib.oracle_radix_digit_source.restype = c.c_uint64
+        lib.oracle_radix_digit_source.argtypes = [c.c_int, c.c_int, c.c_uint64]
+        lib.oracle_radix_sort.restype = c.c_int
+        lib.oracle_radix_sort.argtypes = [c.c_int, c.c_int, c.c_void_p, c.c_void_p,
+                                          c.c_size_t, c.c_size_t, c.c_uint, c.c_uint]
+        lib.oracle_merge.restype = c.c_int
+        lib.oracle_merge.argtypes = [c.c_int, c.c_int, c.c_void_p, c.c_void_p, c.c_size_t,
+                                     c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p,
+                                     c.c_void_p, c.c_size_t]
+        lib.oracle_merge_sort.restype = c.c_int
+        lib.oracle_merge_sort.argtypes = [c.c_int, c.c_int, c.c_void_p, c.c_void_p,
+                                          c.c_size_t, c.c_size_t]
+        lib.oracle_set_op.restype = c.c_longlong
+        lib.oracle_set_op.argtypes = [c.c_int, c.c_int, c.c_int, c.c_void_p, c.c_void_p,
+                                      c.c_size_t, c.c_void_p, c.c_void_p, c.c_size_t,
+                                      c.c_void_p, c.c_void_p, c.c_size_t]
+        _lib = lib
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _vbytes(values):
+    return 0 if values is None else values.dtype.itemsize
+
+
+def splitmix64(x: int) -> int:
+    return _load().oracle_splitmix64(x)
+
+
+def radix_ordered(kind: str, descending: bool, raw: int) -> int:
+    return _load().oracle_radix_ordered(KEY_KINDS[kind], int(descending), raw)
+
+
+def radix_digit_source(kind: str, descending: bool, raw: int) -> int:
+    return _load().oracle_radix_digit_source(KEY_KINDS[kind], int(descending), raw)
+
+
+def radix_sort(kind, keys, values=None, descending=False, begin_bit=0, end_bit=None):
+    keys = np.ascontiguousarray(keys, dtype=KIND_DTYPES[kind]).copy()
+    values = None if values is None else np.ascontiguousarray(values).copy()
+    if end_bit is None:
+        end_bit = keys.dtype.itemsize * 8
+    rc = _load().oracle_radix_sort(KEY_KINDS[kind], int(descending), _ptr(keys), _ptr(values),
+                                   _vbytes(values), keys.size, begin_bit, end_bit)
+    if rc != 0:
+        raise ValueError("invalid radix sort arguments")
+    return (keys, values) if values is not None else keys
+
+
+def merge(kind, a_keys, b_keys, a_values=None, b_values=None, descending=False):
+    dt = KIND_DTYPES[kind]
+    a_keys = np.ascontiguousarray(a_keys, dtype=dt)
+    b_keys = np.ascontiguousarray(b_keys, dtype=dt)
+    out = np.empty(a_keys.size + b_keys.size, dtype=dt)
+    out_v = None
+    if a_values is not None:
+        a_values = np.ascontiguousarray(a_values)
+        b_values = np.ascontiguousarray(b_values, dtype=a_values.dtype)
+        out_v = np.empty(out.size, dtype=a_values.dtype)
+    rc = _load().oracle_merge(KEY_KINDS[kind], int(descending), _ptr(a_keys), _ptr(a_values),
+                              a_keys.size, _ptr(b_keys), _ptr(b_values), b_keys.size,
+                              _ptr(out), _ptr(out_v), _vbytes(a_values))
+    if rc != 0:
+        raise ValueError("invalid merge arguments")
+    return (out, out_v) if out_v is not None else out
+
+
+def merge_sort(kind, keys, values=None, descending=False):
+    keys = np.ascontiguousarray(keys, dtype=KIND_DTYPES[kind]).copy()
+    values = None if values is None else np.ascontiguousarray(values).copy()
+    rc = _load().oracle_merge_sort(KEY_KINDS[kind], int(descending), _ptr(keys), _ptr(values),
+                                   _vbytes(values), keys.size)
+    if rc != 0:
+        raise ValueError("invalid merge sort arguments")
+    return (keys, values) if values is not None else keys
+
+
+def set_op(op, kind, a_keys, b_keys, a_values=None, b_values=None, descending=False,
+           count_only=False):
+    dt = KIND_DTYPES[kind]
+    a_keys = np.ascontiguousarray(a_keys, dtype=dt)
+    b_keys = np.ascontiguousarray(b_keys, dtype=dt)
+    if a_values is not None:
+        a_values = np.ascontiguousarray(a_values)
+    if b_values is not None:
+        b_values = np.ascontiguousarray(b_values, dtype=a_values.dtype)
+    lib = _load()
+    if count_only:
+        n = lib.oracle_set_op(SET_OPS[op], KEY_KINDS[kind], int(descending), _ptr(a_keys), None,
+                              a_keys.size, _ptr(b_keys), None, b_keys.size, None, None, 0)
+        if n < 0:
+            raise ValueError("invalid set operation arguments")
+        return int(n)
+    out = np.empty(a_keys.size + b_keys.size, dtype=dt)
+    out_v = None if a_values is None else np.empty(out.size, dtype=a_values.dtype)
+    n = lib.oracle_set_op(SET_OPS[op], KEY_KINDS[kind], int(descending), _ptr(a_keys),
+                          _ptr(a_values), a_keys.size, _ptr(b_keys), _ptr(b_values),
+                          b_keys.size, _ptr(out), _ptr(out_v), _vbytes(a_values))
+    if n < 0:
+        raise ValueError("invalid set operation arguments")
+    out = out[:n]
+    return (out, out_v[:n]) if out_v is not None else out

@@ -1,0 +1,75 @@
+// Error state, status strings and target check of the rccl_hip C ABI.
+#include <cstring>
+
+#include "common.hpp"
+
+namespace rccl_hip {
+
+namespace {
+thread_local rccl_hip_error_info g_last_error = {RCCL_HIP_SUCCESS, "", 0, 0, 0, 0, 0, 0};
+} // namespace
+
+rccl_hip_status set_error(rccl_hip_status status, const char *role, uint64_t expected,
+                          uint64_t actual) {
+  g_last_error = rccl_hip_error_info{status, role ? role : "", expected, actual, 0, 0, 0, 0};
+  return status;
+}
+
+rccl_hip_status set_bit_range_error(uint32_t begin, uint32_t end, uint32_t key_bits) {
+  g_last_error = rccl_hip_error_info{RCCL_HIP_ERROR_INVALID_BIT_RANGE, "radix bit range", 0, 0,
+                                     begin, end, key_bits, 0};
+  return RCCL_HIP_ERROR_INVALID_BIT_RANGE;
+}
+
+rccl_hip_status set_hip_error(rccl_hip_status status, const char *role, hipError_t err) {
+  g_last_error = rccl_hip_error_info{status, role ? role : "", 0, 0, 0, 0, 0,
+                                     static_cast<int>(err)};
+  return status;
+}
+
+rccl_hip_status ok() { return RCCL_HIP_SUCCESS; }
+
+rccl_hip_status check_launch(const char *role) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_LAUNCH, role, err);
+  return RCCL_HIP_SUCCESS;
+}
+
+} // namespace rccl_hip
+
+extern "C" {
+
+void rccl_hip_last_error(rccl_hip_error_info *info) {
+  if (info) *info = rccl_hip::g_last_error;
+}
+
+const char *rccl_hip_status_string(rccl_hip_status status) {
+  switch (status) {
+  case RCCL_HIP_SUCCESS: return "success";
+  case RCCL_HIP_ERROR_LENGTH_MISMATCH: return "length does not match required length";
+  case RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL: return "workspace is smaller than required";
+  case RCCL_HIP_ERROR_INVALID_BIT_RANGE: return "radix bit range is outside the key or reversed";
+  case RCCL_HIP_ERROR_UNSUPPORTED_TARGET: return "unsupported target: kernels are built for gfx950";
+  case RCCL_HIP_ERROR_SIZE_OVERFLOW: return "combined device range length overflowed";
+  case RCCL_HIP_ERROR_MEMORY: return "device memory error";
+  case RCCL_HIP_ERROR_DRIVER: return "HIP runtime call failed";
+  case RCCL_HIP_ERROR_LAUNCH: return "kernel launch failed";
+  case RCCL_HIP_ERROR_INVALID_ARGUMENT: return "invalid argument";
+  }
+  return "unknown status";
+}
+
+int rccl_hip_abi_version(void) { return RCCL_HIP_ABI_VERSION; }
+
+rccl_hip_status rccl_hip_program_load(int device) {
+  hipDeviceProp_t prop;
+  hipError_t err = hipGetDeviceProperties(&prop, device);
+  if (err != hipSuccess) return rccl_hip::set_hip_error(RCCL_HIP_ERROR_DRIVER, "device properties", err);
+  // gcnArchName looks like "gfx950:sramecc+:xnack-".
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0 ||
+      (prop.gcnArchName[6] != '\0' && prop.gcnArchName[6] != ':'))
+    return rccl_hip::set_error(RCCL_HIP_ERROR_UNSUPPORTED_TARGET, "gfx950 kernels");
+  return rccl_hip::ok();
+}
+
+} // extern "C"

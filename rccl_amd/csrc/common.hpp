@@ -1,0 +1,91 @@
+// Shared host/device helpers for the rccl_hip library (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "rccl_hip.h"
+
+namespace rccl_hip {
+
+// ---------------------------------------------------------------------------
+// Error reporting (host). Mirrors DeviceAlgorithmError's payloads
+// (rccl-cub/src/error.rs:3-25); the last error is kept per thread.
+// ---------------------------------------------------------------------------
+rccl_hip_status set_error(rccl_hip_status status, const char *role = "",
+                          uint64_t expected = 0, uint64_t actual = 0);
+rccl_hip_status set_bit_range_error(uint32_t begin, uint32_t end, uint32_t key_bits);
+rccl_hip_status set_hip_error(rccl_hip_status status, const char *role, hipError_t err);
+rccl_hip_status ok();
+
+#define RCCL_HIP_TRY(expr)                                                      \
+  do {                                                                         \
+    rccl_hip_status rccl_hip_try_status_ = (expr);                             \
+    if (rccl_hip_try_status_ != RCCL_HIP_SUCCESS) return rccl_hip_try_status_; \
+  } while (0)
+
+// Launch check: reports a launch failure as RCCL_HIP_ERROR_LAUNCH.
+rccl_hip_status check_launch(const char *role);
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+inline size_t key_bytes(rccl_hip_key_kind k) {
+  switch (k) {
+  case RCCL_HIP_KEY_U32: case RCCL_HIP_KEY_I32: case RCCL_HIP_KEY_F32: return 4;
+  case RCCL_HIP_KEY_U64: case RCCL_HIP_KEY_I64: case RCCL_HIP_KEY_F64: return 8;
+  case RCCL_HIP_KEY_U8: case RCCL_HIP_KEY_I8: return 1;
+  case RCCL_HIP_KEY_U16: case RCCL_HIP_KEY_I16: return 2;
+  default: return 0;
+  }
+}
+
+inline bool valid_value_bytes(size_t v) {
+  return v == 0 || v == 1 || v == 2 || v == 4 || v == 8 || v == 16;
+}
+
+// Opaque value payloads moved alongside keys.
+struct alignas(16) Value16 {
+  uint32_t w[4];
+};
+
+// ---------------------------------------------------------------------------
+// Device helpers (wave64).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t lane_id() {
+  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
+// Number of set bits of `mask` in lanes below the calling lane.
+__device__ __forceinline__ uint32_t popc_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+// Device-scope (agent) atomics: visible across all XCDs of the GPU.
+template <class T>
+__device__ __forceinline__ T load_agent(const T *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ void store_agent(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T add_agent(T *p, T v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Inclusive scan across the 64 lanes of a wave.
+template <class T>
+__device__ __forceinline__ T wave_inclusive_sum(T v, uint32_t lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    T t = __shfl_up(v, off, 64);
+    if (lane >= static_cast<uint32_t>(off)) v += t;
+  }
+  return v;
+}
+
+} // namespace rccl_hip

@@ -1,0 +1,223 @@
+"""GPU parity tests for DeviceRadixSort through the C ABI.
+
+Cases follow the reference's own probes
+(rccl-cub/examples/device_radix_sort_keys_probe.rs and
+device_radix_sort_pairs_probe.rs); every output is compared bit-for-bit with
+the CPU oracle (oracle/oracle.c) on the same input.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from rccl_amd import cub, workloads
+from rccl_amd.device import DeviceBuffer
+
+pytestmark = pytest.mark.gpu
+
+
+def _sort_keys(launch, host, descending=False):
+    keys = DeviceBuffer.from_host(host)
+    ws = cub.device_radix_sort_workspace(launch, host.dtype, host.size)
+    if descending:
+        cub.device_radix_sort_keys_descending(launch, keys, ws)
+    else:
+        cub.device_radix_sort_keys(launch, keys, ws)
+    launch.synchronize()
+    return keys.to_host_vec()
+
+
+def _sort_pairs(launch, keys_host, values_host, descending=False):
+    keys = DeviceBuffer.from_host(keys_host)
+    values = DeviceBuffer.from_host(values_host)
+    ws = cub.device_radix_sort_pairs_workspace(launch, keys_host.dtype, values_host.dtype,
+                                               keys_host.size)
+    if descending:
+        cub.device_radix_sort_pairs_descending(launch, keys, values, ws)
+    else:
+        cub.device_radix_sort_pairs(launch, keys, values, ws)
+    launch.synchronize()
+    return keys.to_host_vec(), values.to_host_vec()
+
+
+def _kind(a):
+    return {np.dtype(np.uint32): "u32", np.dtype(np.int32): "i32", np.dtype(np.float32): "f32",
+            np.dtype(np.uint64): "u64", np.dtype(np.int64): "i64",
+            np.dtype(np.float64): "f64"}[a.dtype]
+
+
+def _bits(a):
+    return a.view(np.uint32 if a.dtype.itemsize == 4 else np.uint64)
+
+
+def _probe_input_u32(n):
+    # device_radix_sort_keys_probe.rs:36-40
+    i = np.arange(n, dtype=np.uint64)
+    v = (i * np.uint64(2654435761)) & np.uint64(0xFFFFFFFF)
+    r = (i & np.uint64(31))
+    v = ((v << r) | (v >> ((np.uint64(32) - r) & np.uint64(31)))) & np.uint64(0xFFFFFFFF)
+    v = np.where(r == 0, (i * np.uint64(2654435761)) & np.uint64(0xFFFFFFFF), v)
+    return v.astype(np.uint32)
+
+
+def test_empty_and_single(launch):
+    assert _sort_keys(launch, np.empty(0, np.uint32)).size == 0
+    np.testing.assert_array_equal(_sort_keys(launch, np.array([42], np.uint32)), [42])
+
+
+@pytest.mark.parametrize("n", [2, 100, 4864, 4865, 8192, 8193, 10_003, 65_537])
+@pytest.mark.parametrize("descending", [False, True])
+def test_u32_sizes(launch, n, descending):
+    host = _probe_input_u32(n)
+    host[min(17, n - 1)] = 0
+    host[min(29, n - 1)] = 0xFFFFFFFF
+    got = _sort_keys(launch, host, descending)
+    want = oracle.radix_sort("u32", host, descending=descending)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_c1_u32_2pow20(launch):
+    host = workloads.c1_keys()
+    got = _sort_keys(launch, host)
+    np.testing.assert_array_equal(got, np.sort(host))
+    np.testing.assert_array_equal(got, oracle.radix_sort("u32", host))
+
+
+def test_signed_descending_literal(launch):
+    # device_radix_sort_keys_probe.rs:75-97
+    got = _sort_keys(launch, np.array([0, -1, -2**31, 7, -9, 2**31 - 1, -1, 0], np.int32), True)
+    np.testing.assert_array_equal(got, [2**31 - 1, 7, 0, 0, -1, -1, -9, -2**31])
+    got = _sort_keys(launch, np.array([0, -1, -2**63, 7, -9, 2**63 - 1, -1, 0], np.int64), True)
+    np.testing.assert_array_equal(got, [2**63 - 1, 7, 0, 0, -1, -1, -9, -2**63])
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_float_signed_zero_literal(launch, dt):
+    # device_radix_sort_keys_probe.rs:99-119 and :175-199
+    host = np.array([3.0, -0.0, -np.inf, 0.0, -7.5, np.inf], dt)
+    got = _sort_keys(launch, host)
+    want = np.array([-np.inf, -7.5, -0.0, 0.0, 3.0, np.inf], dt)
+    np.testing.assert_array_equal(_bits(got), _bits(want))
+
+
+def test_nan_bit_order_literal(launch):
+    # device_radix_sort_keys_probe.rs:121-173
+    nq, ns, ps, pq = 0xFFC00001, 0xFF800001, 0x7F800001, 0x7FC00001
+    one, mone = 0x3F800000, 0xBF800000
+    host = np.array([pq, one, ns, nq, mone, ps], np.uint32).view(np.float32)
+    asc = _sort_keys(launch, host)
+    np.testing.assert_array_equal(asc.view(np.uint32), [nq, ns, mone, one, ps, pq])
+    desc = _sort_keys(launch, host, True)
+    np.testing.assert_array_equal(desc.view(np.uint32), [pq, ps, one, mone, ns, nq])
+    nq, ns, ps, pq = (0xFFF8000000000001, 0xFFF0000000000001, 0x7FF0000000000001,
+                      0x7FF8000000000001)
+    one, mone = 0x3FF0000000000000, 0xBFF0000000000000
+    host = np.array([pq, one, ns, nq, mone, ps], np.uint64).view(np.float64)
+    asc = _sort_keys(launch, host)
+    np.testing.assert_array_equal(asc.view(np.uint64), [nq, ns, mone, one, ps, pq])
+    desc = _sort_keys(launch, host, True)
+    np.testing.assert_array_equal(desc.view(np.uint64), [pq, ps, one, mone, ns, nq])
+
+
+@pytest.mark.parametrize("descending", [False, True])
+def test_low_entropy_and_uniform(launch, descending):
+    # device_radix_sort_keys_probe.rs:248-294
+    n = (1 << 17) + 3
+    i = np.arange(n, dtype=np.uint64)
+    entropy = ((i * np.uint64(2654435761)) & np.uint64(31)).astype(np.uint32)
+    got = _sort_keys(launch, entropy, descending)
+    want = np.sort(entropy)[::-1] if descending else np.sort(entropy)
+    np.testing.assert_array_equal(got, want)
+    uniform = np.full(n, 4, np.uint32)
+    np.testing.assert_array_equal(_sort_keys(launch, uniform, descending), uniform)
+
+
+@pytest.mark.parametrize("kind", ["u32", "i32", "f32", "u64", "i64", "f64"])
+@pytest.mark.parametrize("descending", [False, True])
+def test_all_kinds_random_bits(launch, kind, descending):
+    n = 50_001
+    dt = np.dtype(oracle.KIND_DTYPES[kind])
+    raw = workloads.hash_range(0xABCDEF + 7 * dt.itemsize, n)
+    if dt.itemsize == 4:
+        host = (raw >> np.uint64(32)).astype(np.uint32).view(dt)
+    else:
+        host = raw.view(dt)
+    host = host.copy()
+    if dt.kind == "f":
+        _bits(host)[::97] = 0
+        _bits(host)[1::89] = 1 << (dt.itemsize * 8 - 1)
+    got = _sort_keys(launch, host, descending)
+    want = oracle.radix_sort(kind, host, descending=descending)
+    np.testing.assert_array_equal(_bits(got), _bits(want))
+
+
+@pytest.mark.parametrize("value_dtype", [np.uint8, np.uint16, np.int32, np.uint64])
+@pytest.mark.parametrize("descending", [False, True])
+def test_pairs_narrow_domain(launch, value_dtype, descending):
+    # device_radix_sort_pairs_probe.rs:33-99: narrow key domain, index values.
+    keys = _probe_input_u32(10_003) & np.uint32(0x3FF)
+    values = np.arange(keys.size).astype(value_dtype)
+    gk, gv = _sort_pairs(launch, keys, values, descending)
+    wk, wv = oracle.radix_sort("u32", keys, values, descending=descending)
+    np.testing.assert_array_equal(gk, wk)
+    np.testing.assert_array_equal(gv, wv)
+
+
+def test_pairs_u64_keys_u32_values(launch):
+    keys, values = workloads.c2_uniform(1 << 18)
+    gk, gv = _sort_pairs(launch, keys, values)
+    wk, wv = oracle.radix_sort("u64", keys, values)
+    np.testing.assert_array_equal(gk, wk)
+    np.testing.assert_array_equal(gv, wv)
+
+
+def test_pairs_float_literal(launch):
+    # device_radix_sort_pairs_probe.rs:177-214
+    keys = np.array([1.25, -0.0, np.inf, -3.5, 0.0, -np.inf], np.float32)
+    values = np.array([4, 2, 5, 1, 3, 0], np.int32)
+    gk, gv = _sort_pairs(launch, keys, values)
+    want = np.array([-np.inf, -3.5, -0.0, 0.0, 1.25, np.inf], np.float32)
+    np.testing.assert_array_equal(gk.view(np.uint32), want.view(np.uint32))
+    np.testing.assert_array_equal(gv, [0, 1, 2, 3, 4, 5])
+
+
+@pytest.mark.parametrize("descending", [False, True])
+def test_window_double_buffer(launch, descending):
+    # device_radix_sort_keys_probe.rs:296-339: bits 0..24 (three passes).
+    i = np.arange(10_003, dtype=np.uint64)
+    low = (i * np.uint64(2654435761)) & np.uint64(0x00FFFFFF)
+    host = (((i & np.uint64(0xFF)) << np.uint64(24)) | low).astype(np.uint32)
+    first = DeviceBuffer.from_host(host)
+    second = DeviceBuffer.zeroed(np.uint32, host.size)
+    buffers = cub.DoubleBuffer.new(first, second)
+    ws = cub.device_radix_sort_keys_buffer_workspace(launch, np.uint32, host.size)
+    if descending:
+        cub.device_radix_sort_keys_buffer_descending(launch, buffers, range(0, 24), ws)
+    else:
+        cub.device_radix_sort_keys_buffer(launch, buffers, range(0, 24), ws)
+    launch.synchronize()
+    got = buffers.current().to_host_vec()
+    field = host & np.uint32(0x00FFFFFF)
+    order = np.argsort(field.astype(np.int64) * (-1 if descending else 1), kind="stable")
+    np.testing.assert_array_equal(got, host[order])
+    np.testing.assert_array_equal(got, oracle.radix_sort("u32", host, descending=descending,
+                                                         begin_bit=0, end_bit=24))
+
+
+def test_window_noop_and_invalid(launch):
+    # device_radix_sort_keys_probe.rs:341-391
+    host = np.array([9, 1, 7, 3], np.uint32)
+    first = DeviceBuffer.from_host(host)
+    second = DeviceBuffer.from_host(np.array([99, 99, 99, 99], np.uint32))
+    buffers = cub.DoubleBuffer.new(first, second)
+    ws = cub.device_radix_sort_keys_buffer_workspace(launch, np.uint32, 4)
+    cub.device_radix_sort_keys_buffer(launch, buffers, range(12, 12), ws)
+    assert buffers.current_is_first()
+    np.testing.assert_array_equal(buffers.current().to_host_vec(), host)
+    with pytest.raises(cub.DeviceAlgorithmError) as err:
+        cub.device_radix_sort_keys_buffer(launch, buffers, range(25, 17), ws)
+    assert err.value.kind == "InvalidBitRange"
+    assert (err.value.begin, err.value.end, err.value.key_bits) == (25, 17, 32)
+    np.testing.assert_array_equal(buffers.current().to_host_vec(), host)
+    cub.device_radix_sort_keys_buffer(launch, buffers, range(0, 8), ws)
+    launch.synchronize()
+    np.testing.assert_array_equal(buffers.current().to_host_vec(), [1, 3, 7, 9])
