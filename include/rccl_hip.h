@@ -115,6 +115,27 @@ RCCL_HIP_API int rccl_hip_abi_version(void);
 RCCL_HIP_API rccl_hip_status rccl_hip_program_load(int device);
 
 /* ------------------------------------------------------------------------
+ * Kernel timing (observability). The reference has no tracing in code; its
+ * benchmarks bracket calls with CUDA events
+ * (rccl-cub/examples/device_ordering_benchmark.rs:29-69). When enabled, the
+ * library records a hipEvent pair around every kernel it launches, on the
+ * launch's stream; rccl_hip_timing_read synchronizes those events, returns
+ * one record per launch in issue order and clears the log.
+ * ------------------------------------------------------------------------ */
+typedef struct rccl_hip_kernel_timing {
+  const char *kernel; /* static name, e.g. "radix_onesweep" */
+  float ms;           /* hipEventElapsedTime of the launch */
+  uint64_t items;     /* items the launch processed */
+} rccl_hip_kernel_timing;
+
+/* Turn per-launch timing on (nonzero) or off (0). Off by default. */
+RCCL_HIP_API rccl_hip_status rccl_hip_timing_enable(int enable);
+/* Copy up to `capacity` records into `out` (may be NULL to query the count),
+ * store the number of records in *count and clear the log. */
+RCCL_HIP_API rccl_hip_status rccl_hip_timing_read(rccl_hip_kernel_timing *out,
+                                                  size_t capacity, size_t *count);
+
+/* ------------------------------------------------------------------------
  * DeviceRadixSort
  * ------------------------------------------------------------------------ */
 

@@ -44,6 +44,8 @@ EXPORTED_SYMBOLS = (
     "rccl_hip_status_string",
     "rccl_hip_abi_version",
     "rccl_hip_program_load",
+    "rccl_hip_timing_enable",
+    "rccl_hip_timing_read",
     "rccl_hip_radix_sort_workspace_bytes",
     "rccl_hip_radix_sort_buffer",
     "rccl_hip_radix_sort",
@@ -66,6 +68,14 @@ class ErrorInfo(ctypes.Structure):
         ("end_bit", ctypes.c_uint32),
         ("key_bits", ctypes.c_uint32),
         ("hip_error", ctypes.c_int),
+    ]
+
+
+class KernelTiming(ctypes.Structure):
+    _fields_ = [
+        ("kernel", ctypes.c_char_p),
+        ("ms", ctypes.c_float),
+        ("items", ctypes.c_uint64),
     ]
 
 
@@ -124,6 +134,10 @@ def _declare(lib):
     lib_view.rccl_hip_abi_version.argtypes = []
     lib_view.rccl_hip_program_load.restype = st
     lib_view.rccl_hip_program_load.argtypes = [c.c_int]
+    lib_view.rccl_hip_timing_enable.restype = st
+    lib_view.rccl_hip_timing_enable.argtypes = [c.c_int]
+    lib_view.rccl_hip_timing_read.restype = st
+    lib_view.rccl_hip_timing_read.argtypes = [c.POINTER(KernelTiming), sz, c.POINTER(sz)]
     lib_view.rccl_hip_radix_sort_workspace_bytes.restype = st
     lib_view.rccl_hip_radix_sort_workspace_bytes.argtypes = [st, sz, sz, c.POINTER(sz)]
     lib_view.rccl_hip_radix_sort_buffer.restype = st
@@ -176,3 +190,18 @@ def workspace_bytes(fn_name: str, *args) -> int:
     out = ctypes.c_size_t(0)
     check(getattr(load(), fn_name)(*args, ctypes.byref(out)))
     return int(out.value)
+
+
+def timing_enable(on: bool) -> None:
+    check(load().rccl_hip_timing_enable(1 if on else 0))
+
+
+def timing_read(capacity: int = 1 << 16) -> list:
+    """Synchronize and return [(kernel, ms, items)] for the launches recorded
+    since the last read (at most `capacity`), clearing the log."""
+    lib = load()
+    buf = (KernelTiming * capacity)()
+    count = ctypes.c_size_t(0)
+    check(lib.rccl_hip_timing_read(buf, capacity, ctypes.byref(count)))
+    n = min(int(count.value), capacity)
+    return [(buf[i].kernel.decode(), float(buf[i].ms), int(buf[i].items)) for i in range(n)]

@@ -20,6 +20,12 @@ INCLUDE = os.path.join(ROOT, "include")
 SOURCES = [
     "abi.hip",
     "radix.hip",
+    "radix_u32.hip",
+    "radix_i32.hip",
+    "radix_f32.hip",
+    "radix_u64.hip",
+    "radix_i64.hip",
+    "radix_f64.hip",
 ]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -1,9 +1,50 @@
 // Error state, status strings and target check of the rccl_hip C ABI.
+#include <atomic>
 #include <cstring>
+#include <mutex>
+#include <vector>
 
 #include "common.hpp"
 
 namespace rccl_hip {
+
+namespace {
+struct TimingRecord {
+  const char *name;
+  hipEvent_t start;
+  hipEvent_t stop;
+  uint64_t items;
+};
+std::atomic<bool> g_timing_on{false};
+std::mutex g_timing_mu;
+std::vector<TimingRecord> g_records;
+std::vector<std::pair<hipEvent_t, hipEvent_t>> g_event_pool;
+} // namespace
+
+KernelTimer::KernelTimer(const char *name, hipStream_t stream, uint64_t items) : stream_(stream) {
+  if (!g_timing_on.load(std::memory_order_relaxed)) return;
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  std::pair<hipEvent_t, hipEvent_t> ev{};
+  if (!g_event_pool.empty()) {
+    ev = g_event_pool.back();
+    g_event_pool.pop_back();
+  } else if (hipEventCreate(&ev.first) != hipSuccess || hipEventCreate(&ev.second) != hipSuccess) {
+    return;
+  }
+  if (hipEventRecord(ev.first, stream) != hipSuccess) {
+    g_event_pool.push_back(ev);
+    return;
+  }
+  g_records.push_back(TimingRecord{name, ev.first, ev.second, items});
+  slot_ = static_cast<int>(g_records.size()) - 1;
+}
+
+KernelTimer::~KernelTimer() {
+  if (slot_ < 0) return;
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  if (slot_ < static_cast<int>(g_records.size()))
+    (void)hipEventRecord(g_records[slot_].stop, stream_);
+}
 
 namespace {
 thread_local rccl_hip_error_info g_last_error = {RCCL_HIP_SUCCESS, "", 0, 0, 0, 0, 0, 0};
@@ -60,6 +101,30 @@ const char *rccl_hip_status_string(rccl_hip_status status) {
 }
 
 int rccl_hip_abi_version(void) { return RCCL_HIP_ABI_VERSION; }
+
+rccl_hip_status rccl_hip_timing_enable(int enable) {
+  rccl_hip::g_timing_on.store(enable != 0);
+  return rccl_hip::ok();
+}
+
+rccl_hip_status rccl_hip_timing_read(rccl_hip_kernel_timing *out, size_t capacity, size_t *count) {
+  if (!count) return rccl_hip::set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "count");
+  std::lock_guard<std::mutex> lock(rccl_hip::g_timing_mu);
+  auto &recs = rccl_hip::g_records;
+  *count = recs.size();
+  rccl_hip_status status = rccl_hip::ok();
+  for (size_t i = 0; i < recs.size(); ++i) {
+    float ms = 0.0f;
+    hipError_t err = hipEventSynchronize(recs[i].stop);
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, recs[i].start, recs[i].stop);
+    if (err != hipSuccess && status == RCCL_HIP_SUCCESS)
+      status = rccl_hip::set_hip_error(RCCL_HIP_ERROR_DRIVER, "kernel timing", err);
+    if (out && i < capacity) out[i] = rccl_hip_kernel_timing{recs[i].name, ms, recs[i].items};
+    rccl_hip::g_event_pool.emplace_back(recs[i].start, recs[i].stop);
+  }
+  recs.clear();
+  return status;
+}
 
 rccl_hip_status rccl_hip_program_load(int device) {
   hipDeviceProp_t prop;

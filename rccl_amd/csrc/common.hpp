@@ -29,6 +29,21 @@ rccl_hip_status ok();
 // Launch check: reports a launch failure as RCCL_HIP_ERROR_LAUNCH.
 rccl_hip_status check_launch(const char *role);
 
+// Per-launch hipEvent timing (rccl_hip_timing_enable). Construct around a
+// launch: records a start event now and a stop event when destroyed, on the
+// launch's stream, only while timing is enabled.
+class KernelTimer {
+public:
+  KernelTimer(const char *name, hipStream_t stream, uint64_t items);
+  ~KernelTimer();
+  KernelTimer(const KernelTimer &) = delete;
+  KernelTimer &operator=(const KernelTimer &) = delete;
+
+private:
+  int slot_ = -1;
+  hipStream_t stream_;
+};
+
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 inline size_t key_bytes(rccl_hip_key_kind k) {

@@ -1,0 +1,681 @@
+// DeviceRadixSort kernels for gfx950: onesweep LSD radix sort, 8-bit digits.
+//
+// Reference behaviour: rccl-cub/src/radix.rs:364-876 (validation and pass
+// control) and rccl-cub/src/ordering_backend/radix.rs (device agents). The
+// kernels are an independent wave64 design:
+//   init        zero the per-pass bins and tile counters (one tiny block)
+//   histogram   one read of all keys builds every pass's 256-bin histogram in
+//               LDS (per-wave private counters) and adds them to the bins; it
+//               also zeroes look-back buffer 0
+//   onesweep    one launch per pass; persistent blocks claim tiles in order,
+//               rank them with wave64 LDS match masks, run a windowed
+//               decoupled look-back on agent-scope atomics, and scatter
+//               through LDS so HBM writes coalesce
+#pragma once
+
+#include <algorithm>
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace rccl_hip {
+namespace radix {
+
+constexpr int BINS = 256;
+
+struct NoValue {};
+
+enum class KeyClass { Unsigned, Signed, Float };
+
+// Order-preserving bit image of a key, with the float +-0 collapse applied
+// for digit extraction. Transforms: rccl-cub/src/ordering_backend/radix.rs:75-235
+// (unsigned identity, signed sign flip, float: negative -> all bits inverted,
+// otherwise sign flipped; descending = complement); collapse: :257-337 (the
+// ordered value 0x7f..f is read as 0x80..0, so -0.0 and +0.0 share every
+// digit). Stored keys are never rewritten.
+template <class Bits, KeyClass KC, bool DESC>
+struct KeyOps {
+  using SBits = typename std::make_signed<Bits>::type;
+  static constexpr int NBITS = int(sizeof(Bits) * 8);
+  static constexpr Bits SIGN = Bits(1) << (NBITS - 1);
+
+  __device__ static __forceinline__ Bits digit_source(Bits raw) {
+    Bits x = raw;
+    if constexpr (KC == KeyClass::Signed) x ^= SIGN;
+    if constexpr (KC == KeyClass::Float)
+      x ^= static_cast<Bits>(static_cast<SBits>(raw) >> (NBITS - 1)) | SIGN;
+    if constexpr (DESC) x = ~x;
+    if constexpr (KC == KeyClass::Float) x = (x == SIGN - 1) ? SIGN : x;
+    return x;
+  }
+
+  __device__ static __forceinline__ uint32_t digit(Bits raw, uint32_t bit, uint32_t mask) {
+    return static_cast<uint32_t>(digit_source(raw) >> bit) & mask;
+  }
+};
+
+// Look-back descriptor: 2 flag bits over a count.
+template <class Desc> struct DescInfo;
+// Flag 3 never appears in memory: it marks a window slot before the start of
+// the tile's look-back group.
+template <> struct DescInfo<uint32_t> {
+  static constexpr int SHIFT = 30;
+  static constexpr uint32_t AGG = 1u << 30, INCL = 2u << 30, BOUNDARY = 3u << 30,
+                            MASK = (1u << 30) - 1;
+};
+template <> struct DescInfo<uint64_t> {
+  static constexpr int SHIFT = 62;
+  static constexpr uint64_t AGG = 1ull << 62, INCL = 2ull << 62, BOUNDARY = 3ull << 62,
+                            MASK = (1ull << 62) - 1;
+};
+
+// Two-level look-back state of one pass. Tiles form groups of GROUP; besides
+// its own descriptor, every tile adds (1 << GAGG_SHIFT) | count to its
+// group's per-digit aggregate word, which is therefore complete exactly when
+// its top byte equals the group size. The group's last tile also publishes
+// the inclusive prefix through the group. A look-back sums in-group
+// predecessors tile by tile and earlier groups whole, so the prefix chain
+// advances a group per step instead of a tile.
+constexpr int GAGG_SHIFT = 24;
+constexpr uint32_t GAGG_MASK = (1u << GAGG_SHIFT) - 1;
+template <class Desc> struct LookbackBuf {
+  Desc *tile;      // tiles x BINS descriptors
+  Desc *ginc;      // groups x BINS inclusive prefixes through each group
+  uint32_t *gagg;  // groups x BINS packed (tiles counted, count)
+};
+
+// ---------------------------------------------------------------------------
+// Policy. Tile = THREADS x ITEMS keys; ITEMS depends on the widest staged
+// element (key or value). Overridable at build time for tuning.
+// ---------------------------------------------------------------------------
+#ifndef RCCL_RADIX_THREADS
+#define RCCL_RADIX_THREADS 512
+#endif
+#ifndef RCCL_RADIX_ITEMS_4B
+#define RCCL_RADIX_ITEMS_4B 24
+#endif
+#ifndef RCCL_RADIX_ITEMS_8B
+#define RCCL_RADIX_ITEMS_8B 12
+#endif
+#ifndef RCCL_RADIX_ITEMS_16B
+#define RCCL_RADIX_ITEMS_16B 8
+#endif
+#ifndef RCCL_RADIX_LOOKBACK_WINDOW
+#define RCCL_RADIX_LOOKBACK_WINDOW 16
+#endif
+#ifndef RCCL_RADIX_WAVES_PER_SIMD
+#define RCCL_RADIX_WAVES_PER_SIMD 4
+#endif
+#ifndef RCCL_RADIX_LOOKBACK_GROUP
+#define RCCL_RADIX_LOOKBACK_GROUP 16
+#endif
+#ifndef RCCL_RADIX_GROUP_WINDOW
+#define RCCL_RADIX_GROUP_WINDOW 4
+#endif
+constexpr int THREADS = RCCL_RADIX_THREADS;
+constexpr int LOOKBACK = RCCL_RADIX_LOOKBACK_WINDOW;
+constexpr int GROUP = RCCL_RADIX_LOOKBACK_GROUP;
+constexpr int GWIN = RCCL_RADIX_GROUP_WINDOW;
+
+constexpr int items_for(size_t elem_bytes) {
+  return elem_bytes <= 4 ? RCCL_RADIX_ITEMS_4B
+                         : (elem_bytes <= 8 ? RCCL_RADIX_ITEMS_8B : RCCL_RADIX_ITEMS_16B);
+}
+constexpr size_t stage_elem(size_t key_bytes, size_t value_bytes) {
+  return key_bytes > value_bytes ? key_bytes : value_bytes;
+}
+inline size_t tile_items(size_t key_bytes, size_t value_bytes) {
+  return size_t(THREADS) * items_for(stage_elem(key_bytes, value_bytes));
+}
+
+// ---------------------------------------------------------------------------
+// init: zero bins and tile counters. (Internal linkage: every translation
+// unit that launches it carries its own copy.)
+// ---------------------------------------------------------------------------
+namespace {
+__global__ void __launch_bounds__(256) init_kernel(uint32_t *bins, uint32_t *counters,
+                                                   uint32_t passes) {
+  for (uint32_t i = threadIdx.x; i < passes * BINS; i += 256) bins[i] = 0;
+  if (threadIdx.x < passes) counters[threadIdx.x] = 0;
+}
+} // namespace
+
+// ---------------------------------------------------------------------------
+// histogram: every pass's digit counts from one read of the keys.
+// ---------------------------------------------------------------------------
+constexpr int HIST_THREADS = 512;
+constexpr int HIST_ITEMS = 16;
+
+template <class Bits, class Ops>
+__global__ void __launch_bounds__(HIST_THREADS)
+histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__ bins,
+                 uint32_t begin_bit, uint32_t end_bit, uint32_t passes,
+                 uint32_t *__restrict__ zero_words, size_t zero_count) {
+  constexpr int WAVES = HIST_THREADS / 64;
+  constexpr int PMAX = sizeof(Bits);
+  __shared__ uint32_t hist[WAVES][PMAX * BINS];
+  const uint32_t tid = threadIdx.x;
+  for (uint32_t i = tid; i < WAVES * PMAX * BINS; i += HIST_THREADS) (&hist[0][0])[i] = 0;
+  for (size_t i = size_t(blockIdx.x) * HIST_THREADS + tid; i < zero_count;
+       i += size_t(gridDim.x) * HIST_THREADS)
+    zero_words[i] = 0;
+  __syncthreads();
+
+  uint32_t *my = hist[tid >> 6];
+  constexpr size_t CHUNK = size_t(HIST_THREADS) * HIST_ITEMS;
+  for (size_t base = size_t(blockIdx.x) * CHUNK; base < n; base += size_t(gridDim.x) * CHUNK) {
+    Bits k[HIST_ITEMS];
+    const uint32_t avail = static_cast<uint32_t>(min<size_t>(n - base, CHUNK));
+#pragma unroll
+    for (int j = 0; j < HIST_ITEMS; ++j) {
+      const uint32_t i = uint32_t(j) * HIST_THREADS + tid;
+      k[j] = i < avail ? keys[base + i] : Bits(0);
+    }
+#pragma unroll
+    for (int j = 0; j < HIST_ITEMS; ++j) {
+      if (uint32_t(j) * HIST_THREADS + tid >= avail) continue;
+      const Bits s = Ops::digit_source(k[j]);
+      for (uint32_t p = 0; p < passes; ++p) {
+        const uint32_t bit = begin_bit + 8u * p;
+        const uint32_t width = min(8u, end_bit - bit);
+        const uint32_t d = static_cast<uint32_t>(s >> bit) & ((1u << width) - 1u);
+        atomicAdd(&my[p * BINS + d], 1u);
+      }
+    }
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < passes * BINS; i += HIST_THREADS) {
+    uint32_t sum = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) sum += hist[w][i];
+    if (sum) add_agent(&bins[i], sum);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// onesweep: one stable counting-sort pass. Persistent blocks claim tiles of
+// THREADS*ITEMS keys in order from an atomic counter and software-pipeline
+// them: the look-back window for tile t is issued right after t's aggregate
+// is published, and the keys of the next tile are loaded before t's
+// look-back is consumed.
+// ---------------------------------------------------------------------------
+template <class Bits, class Val, class Ops, int ITEMS, class Desc>
+__global__ void __launch_bounds__(THREADS, RCCL_RADIX_WAVES_PER_SIMD)
+onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
+                const Val *__restrict__ vals_in, Val *__restrict__ vals_out, size_t n,
+                uint32_t num_tiles, const uint32_t *__restrict__ pass_bins,
+                LookbackBuf<Desc> lbuf, LookbackBuf<Desc> lbuf_next, uint32_t *tile_counter,
+                uint32_t bit, uint32_t mask) {
+  constexpr bool PAIRS = !std::is_same<Val, NoValue>::value;
+  constexpr int WAVES = THREADS / 64;
+  constexpr int TILE = THREADS * ITEMS;
+  constexpr int WAVE_ITEMS = 64 * ITEMS;
+  // Items past the end of the input (last tile only) rank in an extra
+  // dummy bin and stage into one spare slot, so the loops need no branches.
+  constexpr int NB = BINS + 1;
+  constexpr uint32_t DUMMY = BINS;
+  constexpr size_t VAL_BYTES = PAIRS ? sizeof(Val) : 0;
+  constexpr size_t STAGE_ELEM = sizeof(Bits) > VAL_BYTES ? sizeof(Bits) : VAL_BYTES;
+  static_assert(THREADS >= BINS, "one thread per digit is required");
+  static_assert(uint64_t(GROUP) * TILE <= GAGG_MASK, "group counts must fit the packed word");
+  static_assert(LOOKBACK >= 1 && GWIN >= 1, "look-back windows");
+  using DI = DescInfo<Desc>;
+  using ValReg = typename std::conditional<PAIRS, Val, char>::type;
+
+  // The match masks (ranking) and the staged tile (scatter) are never live
+  // at the same time, so they share one LDS buffer.
+  constexpr size_t STAGE_BYTES = (TILE + 1) * STAGE_ELEM;
+  constexpr size_t MATCH_BYTES = size_t(WAVES) * NB * sizeof(uint64_t);
+  __shared__ __attribute__((aligned(16)))
+  unsigned char stage_raw[STAGE_BYTES > MATCH_BYTES ? STAGE_BYTES : MATCH_BYTES];
+  uint64_t(*match)[NB] = reinterpret_cast<uint64_t(*)[NB]>(stage_raw);
+  __shared__ uint32_t hist[WAVES][NB];
+  __shared__ uint32_t digit_off[BINS];
+  __shared__ uint32_t wave_sum[BINS / 64];
+  __shared__ uint32_t s_tile;
+
+  const uint32_t tid0 = threadIdx.x;
+  Bits *stage_keys = reinterpret_cast<Bits *>(stage_raw);
+
+  if (tid0 == 0) s_tile = add_agent(tile_counter, 1u);
+  for (uint32_t i = tid0; i < WAVES * NB; i += THREADS) (&hist[0][0])[i] = 0;
+  // Global start of each digit's bucket: exclusive scan of the pass's bins,
+  // the same for every tile, computed once.
+  uint32_t bin_start = 0;
+  {
+    const uint32_t lane = tid0 & 63u;
+    const uint32_t b = tid0 < BINS ? pass_bins[tid0] : 0u;
+    const uint32_t inc = wave_inclusive_sum(b, lane);
+    if (tid0 < BINS && lane == 63) wave_sum[tid0 >> 6] = inc;
+    __syncthreads();
+    if (tid0 < BINS) {
+      bin_start = inc - b;
+      for (uint32_t w = 0; w < (tid0 >> 6); ++w) bin_start += wave_sum[w];
+    }
+  }
+  uint32_t tile = s_tile;
+  __syncthreads();
+  if (tile >= num_tiles) return;
+
+  // Wave-contiguous, lane-striped load: item j of lane l is key
+  // wave_base + 64 j + l, so (item, lane) order is source order.
+  Bits key[ITEMS];
+  size_t wave_base = size_t(tile) * TILE + size_t(tid0 >> 6) * WAVE_ITEMS;
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const size_t idx = wave_base + size_t(j) * 64 + (tid0 & 63u);
+    key[j] = idx < n ? keys_in[idx] : Bits(0);
+  }
+
+  while (true) {
+    // Values derived from the thread index are recomputed every tile: an
+    // opaque copy keeps the compiler from hoisting dozens of per-item
+    // addresses out of the tile loop into registers.
+    uint32_t tid = tid0;
+    asm volatile("" : "+v"(tid));
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = tid >> 6;
+    // The staging buffer of the previous tile becomes this tile's match
+    // masks: clear them (the end-of-tile barrier has passed).
+    for (uint32_t i = tid; i < WAVES * NB; i += THREADS) (&match[0][0])[i] = 0;
+    __syncthreads();
+    uint64_t *wmatch = match[wave];
+    uint32_t *whist = hist[wave];
+    const uint64_t lane_bit = 1ull << lane;
+    const size_t tile_base = size_t(tile) * TILE;
+    // Items of this wave's chunk that exist (the last tile may be partial).
+    const uint32_t wave_valid =
+        n > wave_base ? static_cast<uint32_t>(min<size_t>(n - wave_base, WAVE_ITEMS)) : 0u;
+
+    ValReg val[ITEMS];
+    if constexpr (PAIRS) {
+      // Issued now, consumed after the key scatter.
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j) {
+        const uint32_t i = uint32_t(j) * 64 + lane;
+        val[j] = i < wave_valid ? vals_in[wave_base + i] : ValReg{};
+      }
+    }
+
+    // Stable rank within the wave. For each item the lanes OR their lane bit
+    // into match[digit]; reading it back gives the peer set, whose popcount
+    // below this lane plus the wave's running digit count is the rank. The
+    // lowest peer advances the count and clears the mask for the next item.
+    // LDS operations of one wave execute in order, so no barrier is needed
+    // between the steps.
+    uint32_t rank[ITEMS];
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      const uint32_t d =
+          uint32_t(j) * 64 + lane < wave_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
+      atomicOr(reinterpret_cast<unsigned long long *>(&wmatch[d]),
+               static_cast<unsigned long long>(lane_bit));
+      __builtin_amdgcn_wave_barrier();
+      const uint64_t peers = wmatch[d];
+      const uint32_t base = whist[d];
+      const uint32_t below = popc_below(peers);
+      rank[j] = base + below;
+      // Keep one register per item (not base and below separately).
+      asm volatile("" : "+v"(rank[j]));
+      __builtin_amdgcn_wave_barrier();
+      if (below == 0) {
+        whist[d] = base + static_cast<uint32_t>(__popcll(peers));
+        wmatch[d] = 0;
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+
+    // Per digit: exclusive prefix over waves and tile total; publish the
+    // aggregate and start the look-back loads at once.
+    uint32_t count = 0;
+    uint32_t tile_inc = 0;
+    const uint32_t group = tile / GROUP;
+    const int gfirst = static_cast<int>(group) * GROUP;
+    Desc lb[LOOKBACK];
+    Desc gi[GWIN];
+    uint32_t ga[GWIN];
+    if (tid < BINS) {
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        const uint32_t c = hist[w][tid];
+        hist[w][tid] = count;
+        count += c;
+      }
+      store_agent(&lbuf.tile[size_t(tile) * BINS + tid],
+                  static_cast<Desc>((tile == 0 ? DI::INCL : DI::AGG) | Desc(count)));
+      add_agent(&lbuf.gagg[size_t(group) * BINS + tid], (1u << GAGG_SHIFT) | count);
+      // Issue both first windows now: in-group predecessors (newest first)
+      // and the groups before this one.
+#pragma unroll
+      for (int w = 0; w < LOOKBACK; ++w) {
+        const int t = static_cast<int>(tile) - 1 - w;
+        lb[w] = t >= gfirst ? load_agent(&lbuf.tile[size_t(t) * BINS + tid]) : DI::BOUNDARY;
+      }
+#pragma unroll
+      for (int w = 0; w < GWIN; ++w) {
+        const int g = static_cast<int>(group) - 1 - w;
+        gi[w] = g >= 0 ? load_agent(&lbuf.ginc[size_t(g) * BINS + tid]) : DI::INCL;
+        ga[w] = g >= 0 ? load_agent(&lbuf.gagg[size_t(g) * BINS + tid]) : 0u;
+      }
+      tile_inc = wave_inclusive_sum(count, lane);
+      if (lane == 63) wave_sum[wave] = tile_inc;
+    }
+    if (tid == 0) s_tile = add_agent(tile_counter, 1u);
+    __syncthreads();
+    const uint32_t next = s_tile;
+    uint32_t tile_start = 0;
+    if (tid < BINS) {
+      tile_start = tile_inc - count;
+      for (uint32_t w = 0; w < wave; ++w) tile_start += wave_sum[w];
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) hist[w][tid] += tile_start;
+    }
+    if (tid < WAVES) hist[tid][DUMMY] = TILE;  // dummy items stage into the spare slot
+    __syncthreads();
+
+    // Stage keys in digit order. The empty asm statements stop the compiler
+    // from keeping per-item digit addresses alive from the ranking loop
+    // (recomputing them is cheaper than the registers).
+    uint32_t slane = lane;
+    asm volatile("" : "+v"(slane));
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) asm volatile("" : "+v"(key[j]));
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      const uint32_t d =
+          uint32_t(j) * 64 + slane < wave_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
+      rank[j] = min(rank[j] + whist[d], uint32_t(TILE));
+      stage_keys[rank[j]] = key[j];
+    }
+
+    // Prefetch the next tile's keys (the current keys are dead now); they
+    // land while this tile's look-back and scatter run.
+    Bits nkey[ITEMS];
+    const size_t next_wave_base = size_t(next) * TILE + size_t(wave) * WAVE_ITEMS;
+    if (next < num_tiles) {
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j) {
+        const size_t idx = next_wave_base + size_t(j) * 64 + lane;
+        nkey[j] = idx < n ? keys_in[idx] : Bits(0);
+      }
+    }
+
+    // Two-level decoupled look-back, one thread per digit, consuming the
+    // windows issued above newest first. In-group predecessors are summed
+    // tile by tile until an inclusive prefix or the group start; earlier
+    // groups are then summed whole (complete aggregates) until a group's
+    // inclusive prefix. A slot that is not yet published is polled again.
+    if (tid < BINS) {
+      Desc excl = 0;
+      bool done = tile == 0;
+      int t = static_cast<int>(tile) - 1;
+      while (!done) {
+        int consumed = 0;
+        bool stop = false;
+#pragma unroll
+        for (int w = 0; w < LOOKBACK; ++w) {
+          if (!done && !stop) {
+            const Desc flag = lb[w] >> DI::SHIFT;
+            if (flag == 0 || flag == (DI::BOUNDARY >> DI::SHIFT)) {
+              stop = true;
+            } else {
+              excl += lb[w] & DI::MASK;
+              ++consumed;
+              done = flag == (DI::INCL >> DI::SHIFT);
+            }
+          }
+        }
+        if (done) break;
+        t -= consumed;
+        if (t < gfirst) break;  // every in-group predecessor summed
+        if (consumed == 0) __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int w = 0; w < LOOKBACK; ++w)
+          lb[w] = t - w >= gfirst ? load_agent(&lbuf.tile[size_t(t - w) * BINS + tid])
+                                  : DI::BOUNDARY;
+      }
+      int g = static_cast<int>(group) - 1;
+      while (!done) {
+        int consumed = 0;
+        bool blocked = false;
+#pragma unroll
+        for (int w = 0; w < GWIN; ++w) {
+          if (!done && !blocked) {
+            if ((gi[w] >> DI::SHIFT) == (DI::INCL >> DI::SHIFT)) {
+              excl += gi[w] & DI::MASK;
+              done = true;
+            } else if ((ga[w] >> GAGG_SHIFT) == uint32_t(GROUP)) {
+              excl += ga[w] & GAGG_MASK;  // earlier groups are always full
+              ++consumed;
+            } else {
+              blocked = true;
+            }
+          }
+        }
+        if (done) break;
+        g -= consumed;
+        if (consumed == 0) __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int w = 0; w < GWIN; ++w) {
+          const int gg = g - w;
+          gi[w] = gg >= 0 ? load_agent(&lbuf.ginc[size_t(gg) * BINS + tid]) : DI::INCL;
+          ga[w] = gg >= 0 ? load_agent(&lbuf.gagg[size_t(gg) * BINS + tid]) : 0u;
+        }
+      }
+      const Desc incl = static_cast<Desc>(DI::INCL | (excl + Desc(count)));
+      if (tile > 0) store_agent(&lbuf.tile[size_t(tile) * BINS + tid], incl);
+      const uint32_t glast = min(uint32_t(gfirst + GROUP), num_tiles) - 1u;
+      if (tile == glast) store_agent(&lbuf.ginc[size_t(group) * BINS + tid], incl);
+      digit_off[tid] = bin_start + static_cast<uint32_t>(excl) - tile_start;
+    }
+    __syncthreads();
+    // hist is free until the next tile's ranking: clear it now.
+    for (uint32_t i = tid; i < WAVES * NB; i += THREADS) (&hist[0][0])[i] = 0;
+
+    // Coalesced scatter: consecutive staged keys of one digit go to
+    // consecutive output positions.
+    const uint32_t valid_count = static_cast<uint32_t>(min<size_t>(TILE, n - tile_base));
+    // Positions are exact when the bins match the keys; the clamp only keeps
+    // a caller that changes the keys mid-sort from writing out of bounds.
+    const uint32_t last = static_cast<uint32_t>(n - 1);
+    uint32_t dst[PAIRS ? ITEMS : 1];
+    if (valid_count == TILE) {
+#pragma unroll
+      for (int k = 0; k < ITEMS; ++k) {
+        const uint32_t i = uint32_t(k) * THREADS + tid;
+        const Bits kk = stage_keys[i];
+        const uint32_t p = min(digit_off[Ops::digit(kk, bit, mask)] + i, last);
+        keys_out[p] = kk;
+        if constexpr (PAIRS) dst[k] = p;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < ITEMS; ++k) {
+        const uint32_t i = uint32_t(k) * THREADS + tid;
+        if (i < valid_count) {
+          const Bits kk = stage_keys[i];
+          const uint32_t p = min(digit_off[Ops::digit(kk, bit, mask)] + i, last);
+          keys_out[p] = kk;
+          if constexpr (PAIRS) dst[k] = p;
+        }
+      }
+    }
+    if constexpr (PAIRS) {
+      __syncthreads();
+      Val *stage_vals = reinterpret_cast<Val *>(stage_raw);
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j) stage_vals[rank[j]] = val[j];
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < ITEMS; ++k) {
+        const uint32_t i = uint32_t(k) * THREADS + tid;
+        if (i < valid_count) vals_out[dst[k]] = stage_vals[i];
+      }
+    }
+    if (tid < BINS && lbuf_next.tile) {
+      lbuf_next.tile[size_t(tile) * BINS + tid] = 0;
+      if (static_cast<int>(tile) == gfirst) {
+        lbuf_next.ginc[size_t(group) * BINS + tid] = 0;
+        lbuf_next.gagg[size_t(group) * BINS + tid] = 0;
+      }
+    }
+    __syncthreads();
+
+    if (next >= num_tiles) break;
+    tile = next;
+    wave_base = next_wave_base;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) key[j] = nkey[j];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+
+// Largest item count the control words support: 30-bit look-back counts
+// switch to 62-bit descriptors at 2^30; positions are 32-bit.
+constexpr uint64_t MAX_ITEMS = 0xffffffffull;
+
+struct Layout {
+  size_t tiles = 0;
+  size_t groups = 0;
+  size_t desc_bytes = 4;
+  size_t bins = 0, counters = 0;
+  size_t lb[2] = {0, 0};  // look-back buffers: tile descriptors, group prefixes, aggregates
+  size_t lb_ginc = 0, lb_gagg = 0, lb_bytes = 0;  // offsets/size within one buffer
+  size_t total = 0;
+};
+
+Layout layout(size_t key_bytes, size_t value_bytes, size_t n);
+
+struct SortArgs {
+  void *keys[2];
+  void *vals[2];
+  size_t n;
+  int cur;  // index of the buffer holding the input
+  uint32_t begin_bit, end_bit;
+  unsigned char *ws;
+  hipStream_t stream;
+};
+
+template <class Bits, class Val, class Ops, class Desc>
+rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
+  constexpr int ITEMS =
+      items_for(stage_elem(sizeof(Bits), std::is_same<Val, NoValue>::value ? 0 : sizeof(Val)));
+  uint32_t *bins = reinterpret_cast<uint32_t *>(a.ws + l.bins);
+  uint32_t *counters = reinterpret_cast<uint32_t *>(a.ws + l.counters);
+  LookbackBuf<Desc> lb[2];
+  for (int b = 0; b < 2; ++b) {
+    unsigned char *base = a.ws + l.lb[b];
+    lb[b].tile = reinterpret_cast<Desc *>(base);
+    lb[b].ginc = reinterpret_cast<Desc *>(base + l.lb_ginc);
+    lb[b].gagg = reinterpret_cast<uint32_t *>(base + l.lb_gagg);
+  }
+
+  {
+    KernelTimer t("radix_init", a.stream, 0);
+    init_kernel<<<1, 256, 0, a.stream>>>(bins, counters, passes);
+  }
+  RCCL_HIP_TRY(check_launch("radix init"));
+
+  const size_t chunk = size_t(HIST_THREADS) * HIST_ITEMS;
+  const size_t hist_blocks = std::max<size_t>(1, std::min<size_t>((a.n + chunk - 1) / chunk, 2048));
+  const size_t zero_words = l.lb_bytes / sizeof(uint32_t);
+  {
+    KernelTimer t("radix_histogram", a.stream, a.n);
+    histogram_kernel<Bits, Ops><<<dim3(static_cast<uint32_t>(hist_blocks)), HIST_THREADS, 0,
+                                  a.stream>>>(
+        static_cast<const Bits *>(a.keys[a.cur]), a.n, bins, a.begin_bit, a.end_bit, passes,
+        reinterpret_cast<uint32_t *>(a.ws + l.lb[0]), zero_words);
+  }
+  RCCL_HIP_TRY(check_launch("radix histogram"));
+
+  // Persistent grid: as many blocks as fit on the device at once, but never
+  // more than there are tiles.
+  static int blocks_per_cu = 0;
+  static int cus = 0;
+  if (blocks_per_cu == 0) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err == hipSuccess)
+      err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err == hipSuccess)
+      err = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &blocks_per_cu, onesweep_kernel<Bits, Val, Ops, ITEMS, Desc>, THREADS, 0);
+    if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "radix occupancy", err);
+    if (blocks_per_cu < 1 || cus < 1)
+      return set_error(RCCL_HIP_ERROR_LAUNCH, "radix onesweep does not fit on the device");
+  }
+  const uint32_t grid =
+      static_cast<uint32_t>(std::min<size_t>(l.tiles, size_t(blocks_per_cu) * size_t(cus)));
+
+  for (uint32_t p = 0; p < passes; ++p) {
+    const uint32_t bit = a.begin_bit + 8u * p;
+    const uint32_t width = std::min(8u, a.end_bit - bit);
+    const uint32_t mask = (1u << width) - 1u;
+    const int in = a.cur, out = 1 - a.cur;
+    KernelTimer t("radix_onesweep", a.stream, a.n);
+    onesweep_kernel<Bits, Val, Ops, ITEMS, Desc><<<dim3(grid), THREADS, 0, a.stream>>>(
+        static_cast<const Bits *>(a.keys[in]), static_cast<Bits *>(a.keys[out]),
+        static_cast<const Val *>(a.vals[in]), static_cast<Val *>(a.vals[out]), a.n,
+        static_cast<uint32_t>(l.tiles), bins + size_t(p) * BINS, lb[p & 1],
+        p + 1 < passes ? lb[(p + 1) & 1] : LookbackBuf<Desc>{nullptr, nullptr, nullptr},
+        counters + p, bit, mask);
+    RCCL_HIP_TRY(check_launch("radix onesweep"));
+    a.cur = out;
+  }
+  return ok();
+}
+
+template <class Bits, class Ops>
+rccl_hip_status run_values(SortArgs &a, size_t value_bytes, const Layout &l, uint32_t passes) {
+  const bool wide = l.desc_bytes == 8;
+  switch (value_bytes) {
+  case 0:
+    return wide ? run_passes<Bits, NoValue, Ops, uint64_t>(a, l, passes)
+                : run_passes<Bits, NoValue, Ops, uint32_t>(a, l, passes);
+  case 1:
+    return wide ? run_passes<Bits, uint8_t, Ops, uint64_t>(a, l, passes)
+                : run_passes<Bits, uint8_t, Ops, uint32_t>(a, l, passes);
+  case 2:
+    return wide ? run_passes<Bits, uint16_t, Ops, uint64_t>(a, l, passes)
+                : run_passes<Bits, uint16_t, Ops, uint32_t>(a, l, passes);
+  case 4:
+    return wide ? run_passes<Bits, uint32_t, Ops, uint64_t>(a, l, passes)
+                : run_passes<Bits, uint32_t, Ops, uint32_t>(a, l, passes);
+  case 8:
+    return wide ? run_passes<Bits, uint64_t, Ops, uint64_t>(a, l, passes)
+                : run_passes<Bits, uint64_t, Ops, uint32_t>(a, l, passes);
+  case 16:
+    return wide ? run_passes<Bits, Value16, Ops, uint64_t>(a, l, passes)
+                : run_passes<Bits, Value16, Ops, uint32_t>(a, l, passes);
+  }
+  return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix value bytes");
+}
+
+// One entry per key kind, each compiled in its own translation unit.
+#define RCCL_RADIX_DECLARE_KIND(NAME)                                                   \
+  rccl_hip_status run_##NAME(SortArgs &a, size_t value_bytes, const Layout &l,         \
+                             uint32_t passes, bool descending);
+RCCL_RADIX_DECLARE_KIND(u32)
+RCCL_RADIX_DECLARE_KIND(i32)
+RCCL_RADIX_DECLARE_KIND(f32)
+RCCL_RADIX_DECLARE_KIND(u64)
+RCCL_RADIX_DECLARE_KIND(i64)
+RCCL_RADIX_DECLARE_KIND(f64)
+#undef RCCL_RADIX_DECLARE_KIND
+
+#define RCCL_RADIX_DEFINE_KIND(NAME, BITS, CLASS)                                       \
+  rccl_hip_status run_##NAME(SortArgs &a, size_t value_bytes, const Layout &l,         \
+                             uint32_t passes, bool descending) {                       \
+    return descending                                                                  \
+               ? run_values<BITS, KeyOps<BITS, KeyClass::CLASS, true>>(a, value_bytes, l, \
+                                                                       passes)         \
+               : run_values<BITS, KeyOps<BITS, KeyClass::CLASS, false>>(a, value_bytes, \
+                                                                        l, passes);    \
+  }
+
+} // namespace radix
+} // namespace rccl_hip
