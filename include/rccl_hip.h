@@ -231,11 +231,14 @@ RCCL_HIP_API rccl_hip_status rccl_hip_set_op_workspace_bytes(rccl_hip_set_operat
                                                 size_t *bytes);
 
 /* Sorted multiset operation. Writes the result length to *d_out_count
- * (device memory, one uint64_t). out_keys == NULL counts without writing
- * keys (the `.count()` form); out_values is NULL iff value_bytes == 0 or
- * out_keys == NULL. For INTERSECTION b_values is not read. The output buffers
- * must hold the operation's maximum output (union/symmetric difference:
- * na + nb; intersection: min(na, nb); difference: na).
+ * (device memory, one uint64_t; may be NULL when out_keys is given).
+ * out_keys == NULL counts without writing keys (the `.count()` form; then
+ * d_out_count is required); out_values is read only when value_bytes != 0
+ * and out_keys != NULL. INTERSECTION and DIFFERENCE emit values from A only
+ * and do not read b_values. Empty inputs write a count of 0. out_capacity is
+ * the number of items out_keys (and out_values) can hold: the full result
+ * length is always counted, but items at or past out_capacity are not
+ * written (the reference leaves the destination's size to the caller).
  * Replaces Launch::set_keys / set_pairs (rccl-cub/src/dispatch.rs:413-550;
  * rccl-cub/src/set_operation.rs:265-589) and the Thrust union/intersection/
  * difference/symmetric_difference expressions (rccl-thrust/src/set.rs:357-898). */
@@ -243,9 +246,9 @@ RCCL_HIP_API rccl_hip_status rccl_hip_set_op(rccl_hip_set_operation op, rccl_hip
                                 size_t value_bytes, rccl_hip_order order,
                                 const void *a_keys, const void *a_values, size_t na,
                                 const void *b_keys, const void *b_values, size_t nb,
-                                void *out_keys, void *out_values, uint64_t *d_out_count,
-                                void *workspace, size_t workspace_bytes,
-                                hipStream_t stream);
+                                void *out_keys, void *out_values, size_t out_capacity,
+                                uint64_t *d_out_count, void *workspace,
+                                size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

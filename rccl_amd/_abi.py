@@ -156,7 +156,8 @@ def _declare(lib):
     lib_view.rccl_hip_set_op_workspace_bytes.restype = st
     lib_view.rccl_hip_set_op_workspace_bytes.argtypes = [st, st, sz, sz, sz, c.POINTER(sz)]
     lib_view.rccl_hip_set_op.restype = st
-    lib_view.rccl_hip_set_op.argtypes = [st, st, sz, st, vp, vp, sz, vp, vp, sz, vp, vp, vp, vp, sz, vp]
+    lib_view.rccl_hip_set_op.argtypes = [st, st, sz, st, vp, vp, sz, vp, vp, sz, vp, vp, sz, vp, vp,
+                                         sz, vp]
 
 
 def load():

@@ -17,16 +17,7 @@ BUILD_DIR = os.path.join(HERE, "_build")
 LIB_PATH = os.path.join(HERE, "librccl_hip.so")
 INCLUDE = os.path.join(ROOT, "include")
 
-SOURCES = [
-    "abi.hip",
-    "radix.hip",
-    "radix_u32.hip",
-    "radix_i32.hip",
-    "radix_f32.hip",
-    "radix_u64.hip",
-    "radix_i64.hip",
-    "radix_f64.hip",
-]
+SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

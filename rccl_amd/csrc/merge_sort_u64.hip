@@ -1,0 +1,8 @@
+// DeviceMergeSort instantiation for u64 keys (both orders, every value width).
+#include "merge_sort_kernels.hpp"
+
+namespace rccl_hip {
+namespace merge_sort {
+RCCL_MERGE_SORT_DEFINE_KIND(u64, uint64_t)
+} // namespace merge_sort
+} // namespace rccl_hip

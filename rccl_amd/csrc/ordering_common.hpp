@@ -1,0 +1,90 @@
+// Shared pieces of the comparison-based ordering kernels (merge, merge sort,
+// set operations): key comparators, value payload types, and the dispatch of
+// a runtime (key kind, order, value width) onto compile-time instantiations.
+#pragma once
+
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace rccl_hip {
+namespace ordering {
+
+struct NoValue {};
+
+// Natural order of the key type, or its reverse. Floats compare with IEEE
+// `<`, so -0.0 and +0.0 are equivalent. This is the closure-free natural
+// order of rccl-thrust/src/merge.rs:169-178 (Less iff a < b, Greater iff
+// b < a, else Equal) and its reversal `|a, b| b.cmp(a)`.
+template <class K, bool DESC>
+struct Less {
+  __device__ __forceinline__ bool operator()(const K &a, const K &b) const {
+    if constexpr (DESC) return b < a;
+    else return a < b;
+  }
+};
+
+template <class T>
+__device__ __forceinline__ T load_or(const T *p, size_t i, size_t n, T fallback) {
+  return i < n ? p[i] : fallback;
+}
+
+// Merge-path split of diagonal `diag` between sorted A[0, na) and
+// B[0, nb): the number of A items among the first `diag` merged outputs.
+// B moves ahead only when strictly before A, so equal keys take A first
+// (rccl-memory/src/device.rs:25-71, rccl-cub/src/ordering_backend/merge.rs:16-24).
+template <class K, class Cmp, class ReadA, class ReadB>
+__device__ __forceinline__ size_t merge_path(ReadA a, size_t na, ReadB b, size_t nb, size_t diag,
+                                             Cmp less) {
+  size_t lo = diag > nb ? diag - nb : 0;
+  size_t hi = diag < na ? diag : na;
+  while (lo < hi) {
+    const size_t mid = lo + (hi - lo) / 2;
+    if (less(b(diag - 1 - mid), a(mid)))
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  return lo;
+}
+
+// 32-bit variant for LDS-resident slices.
+template <class K, class Cmp>
+__device__ __forceinline__ uint32_t merge_path_lds(const K *a, uint32_t na, const K *b, uint32_t nb,
+                                                   uint32_t diag, Cmp less) {
+  uint32_t lo = diag > nb ? diag - nb : 0u;
+  uint32_t hi = diag < na ? diag : na;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (less(b[diag - 1 - mid], a[mid]))
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  return lo;
+}
+
+// Padded LDS index for blocked <-> striped transposes: one pad slot after
+// every ITEMS items makes a thread's blocked run start ITEMS + 1 slots after
+// its neighbour's, so both access patterns spread over the banks.
+template <int ITEMS>
+__device__ __forceinline__ uint32_t padded(uint32_t i) {
+  return i + i / ITEMS;
+}
+constexpr uint32_t padded_size(uint32_t n, uint32_t items) { return n + n / items + 1; }
+
+} // namespace ordering
+
+// Runtime value width -> RUNNER::run<V>(args...) (RUNNER is a type name).
+#define RCCL_ORDERING_DISPATCH_VALUE(VB, RUNNER, ...)                                    \
+  switch (VB) {                                                                          \
+  case 0: return RUNNER::run<ordering::NoValue>(__VA_ARGS__);                            \
+  case 1: return RUNNER::run<uint8_t>(__VA_ARGS__);                                      \
+  case 2: return RUNNER::run<uint16_t>(__VA_ARGS__);                                     \
+  case 4: return RUNNER::run<uint32_t>(__VA_ARGS__);                                     \
+  case 8: return RUNNER::run<uint64_t>(__VA_ARGS__);                                     \
+  case 16: return RUNNER::run<Value16>(__VA_ARGS__);                                     \
+  default: break;                                                                        \
+  }
+
+} // namespace rccl_hip

@@ -1,0 +1,488 @@
+// Sorted multiset operations for gfx950: union, intersection, difference and
+// symmetric difference (keys or key/value pairs, or a count only).
+//
+// Reference behaviour: rccl-cub/src/set_operation.rs:265-589 (host control)
+// and rccl-cub/src/ordering_backend/set.rs (agents): balanced-path
+// partitioning (:401-506), the four serial operations (:564-827), tile
+// compaction with decoupled look-back and the final count (:830-1546).
+// Design:
+//   partition  one thread per tile boundary: balanced path in HBM
+//   tile       one block per tile: A and B slices staged in LDS, a balanced
+//              path per thread in LDS, ITEMS steps of the serial operation,
+//              a block scan of the emitted counts, a two-level decoupled
+//              look-back for the tile's global output offset (a whole wave
+//              polls 64 predecessors at once), LDS-compacted coalesced
+//              stores; the last tile writes the output count
+#pragma once
+
+#include <algorithm>
+
+#include "ordering_common.hpp"
+
+namespace rccl_hip {
+namespace set_ops {
+
+using ordering::NoValue;
+
+constexpr int THREADS = 256;
+constexpr int WAVES = THREADS / 64;
+constexpr int GROUP = 64;  // tiles per look-back group (one wave polls a group)
+
+enum Op : int { UNION = 0, INTERSECTION = 1, DIFFERENCE = 2, SYMMETRIC_DIFFERENCE = 3 };
+
+template <class K, class V>
+constexpr int items_for() {
+  constexpr size_t bytes = sizeof(K) + (std::is_same<V, NoValue>::value ? 0 : sizeof(V));
+  return bytes <= 8 ? 16 : (bytes <= 16 ? 12 : 8);
+}
+template <class K, class V>
+constexpr size_t tile_items() {
+  return size_t(THREADS) * items_for<K, V>();
+}
+
+// Look-back words: 2 flag bits over a 62-bit count.
+constexpr uint64_t F_AGG = 1ull << 62, F_INCL = 2ull << 62, VMASK = (1ull << 62) - 1;
+// Group aggregate: tiles counted in the top 16 bits, count below.
+constexpr int GA_SHIFT = 48;
+constexpr uint64_t GA_MASK = (1ull << GA_SHIFT) - 1;
+
+// Balanced path at `diag` (rccl-cub/src/ordering_backend/set.rs:436-506): the
+// merge-path split, moved inside a run of keys equal to B[j] so that the run's
+// A and B items are divided evenly and each A item stays on the side of its
+// B partner; `star` adds the partner of a trailing unmatched A item to this
+// side. Returns (i, j) with i + j = diag + star.
+template <class K, class Cmp, class RA, class RB>
+__device__ __forceinline__ void balanced_path(RA a, size_t na, RB b, size_t nb, size_t diag,
+                                              Cmp less, size_t &out_i, size_t &out_j) {
+  size_t i = ordering::merge_path<K>(a, na, b, nb, diag, less);
+  const size_t j = diag - i;
+  size_t star = 0;
+  if (j < nb) {
+    const K key = b(j);
+    size_t lo = 0, hi = i;  // first A in [0, i) not before key
+    while (lo < hi) {
+      const size_t mid = lo + (hi - lo) / 2;
+      if (less(a(mid), key)) lo = mid + 1; else hi = mid;
+    }
+    const size_t i_start = lo;
+    lo = 0;
+    hi = j;  // first B in [0, j) not before key
+    while (lo < hi) {
+      const size_t mid = lo + (hi - lo) / 2;
+      if (less(b(mid), key)) lo = mid + 1; else hi = mid;
+    }
+    const size_t j_start = lo;
+    const size_t a_run = i - i_start;
+    const size_t b_seen = j - j_start;
+    const size_t total = a_run + b_seen;
+    size_t b_adv = std::max(total >> 1, b_seen);
+    const size_t b_end = std::min(nb, j_start + b_adv + 1);
+    lo = j;
+    hi = b_end;  // end of the key's B run within [j, b_end)
+    while (lo < hi) {
+      const size_t mid = lo + (hi - lo) / 2;
+      if (!less(key, b(mid))) lo = mid + 1; else hi = mid;
+    }
+    const size_t b_run = lo - j_start;
+    b_adv = std::min(b_adv, b_run);
+    const size_t a_adv = total - b_adv;
+    star = (a_adv == b_adv + 1 && b_adv < b_run) ? 1 : 0;
+    i = i_start + a_adv;
+  }
+  out_i = i;
+  out_j = diag - i + star;
+}
+
+template <class K, class Cmp>
+__global__ void __launch_bounds__(256)
+partition_kernel(const K *__restrict__ a, size_t na, const K *__restrict__ b, size_t nb,
+                 size_t tile, size_t count, uint64_t *__restrict__ splits) {
+  const size_t t = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= count) return;
+  const size_t diag = std::min(t * tile, na + nb);
+  size_t i, j;
+  balanced_path<K>([&](size_t x) { return a[x]; }, na, [&](size_t x) { return b[x]; }, nb, diag,
+                   Cmp{}, i, j);
+  splits[2 * t] = i;
+  splits[2 * t + 1] = j;
+}
+
+// Zero the look-back state (tile descriptors, group aggregates and inclusive
+// prefixes) before a launch (one copy per translation unit).
+namespace {
+__global__ void __launch_bounds__(256) clear_kernel(uint64_t *p, size_t words) {
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < words; i += size_t(gridDim.x) * 256)
+    p[i] = 0;
+}
+} // namespace
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <class K, class V, int ITEMS>
+struct TileSmem {
+  static constexpr uint32_t TILE = THREADS * ITEMS;
+  static constexpr uint32_t CAP = TILE + 2;  // a star can make a tile one item longer
+  static constexpr bool PAIRS = !std::is_same<V, NoValue>::value;
+  K keys[CAP];
+  typename std::conditional<PAIRS, V, char>::type vals[PAIRS ? CAP : 1];
+  uint32_t split_a[THREADS + 1];
+  uint32_t split_b[THREADS + 1];
+  uint32_t wave_total[WAVES];
+  uint64_t tile_offset;
+};
+
+// One serial step of operation OP on the current heads. Mirrors the four
+// serial operations of rccl-cub/src/ordering_backend/set.rs:564-827:
+//   union         emit B if B < A, else emit A (equal heads: A, both advance)
+//   intersection  emit A when the heads are equal
+//   difference    emit A when A < B (or B is exhausted)
+//   symmetric     emit the strictly smaller head (or the remaining side)
+// `emit_b` selects the source of the emitted item.
+template <int OP, class K, class Cmp>
+__device__ __forceinline__ void serial_step(const K &ka, const K &kb, bool a_ok, bool b_ok,
+                                            Cmp less, bool &emit, bool &emit_b, bool &adv_a,
+                                            bool &adv_b) {
+  bool a_sel, b_sel;
+  if (!a_ok) {
+    b_sel = true;
+    a_sel = false;
+  } else if (!b_ok) {
+    a_sel = true;
+    b_sel = false;
+  } else {
+    a_sel = less(ka, kb);
+    b_sel = !a_sel && less(kb, ka);
+  }
+  const bool live = a_ok || b_ok;
+  if constexpr (OP == INTERSECTION) {
+    emit = a_ok && b_ok && !a_sel && !b_sel;
+    emit_b = false;
+  } else if constexpr (OP == UNION) {
+    emit = live;
+    emit_b = b_sel;
+  } else if constexpr (OP == DIFFERENCE) {
+    emit = live && a_sel;
+    emit_b = false;
+  } else {
+    emit = live && (a_sel != b_sel);
+    emit_b = b_sel;
+  }
+  adv_a = live && !b_sel;
+  adv_b = live && !a_sel;
+}
+
+template <class K, class V, class Cmp, int OP, int ITEMS>
+__global__ void __launch_bounds__(THREADS)
+tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restrict__ b,
+            const V *__restrict__ bv, const uint64_t *__restrict__ splits, size_t tiles,
+            K *__restrict__ out, V *__restrict__ outv, size_t out_cap,
+            uint64_t *__restrict__ out_count, uint64_t *desc, uint64_t *gagg, uint64_t *ginc) {
+  using Smem = TileSmem<K, V, ITEMS>;
+  constexpr bool PAIRS = Smem::PAIRS;
+  constexpr bool VALS_B = PAIRS && (OP == UNION || OP == SYMMETRIC_DIFFERENCE);
+  __shared__ Smem sm;
+  const Cmp less{};
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave = tid >> 6;
+  const size_t t = blockIdx.x;
+  const size_t i0 = splits[2 * t], j0 = splits[2 * t + 1];
+  const size_t i1 = splits[2 * t + 2], j1 = splits[2 * t + 3];
+  const uint32_t la = static_cast<uint32_t>(i1 - i0);
+  const uint32_t lb = static_cast<uint32_t>(j1 - j0);
+  const uint32_t len = la + lb;
+
+  // Stage A then B (striped, coalesced).
+  for (uint32_t i = tid; i < len; i += THREADS) {
+    sm.keys[i] = i < la ? a[i0 + i] : b[j0 + (i - la)];
+    if constexpr (PAIRS) {
+      if (i < la) sm.vals[i] = av[i0 + i];
+      else if constexpr (VALS_B) sm.vals[i] = bv[j0 + (i - la)];
+    }
+  }
+  __syncthreads();
+
+  // Per-thread balanced-path splits (diagonal tid * ITEMS of this tile).
+  {
+    const K *ka = sm.keys;
+    const K *kb = sm.keys + la;
+    size_t si, sj;
+    const uint32_t diag = min(tid * uint32_t(ITEMS), len);
+    balanced_path<K>([&](size_t x) { return ka[x]; }, la, [&](size_t x) { return kb[x]; }, lb,
+                     diag, less, si, sj);
+    // Every split lies inside the tile; the star of a diagonal past the end
+    // is clamped.
+    sm.split_a[tid] = static_cast<uint32_t>(min<size_t>(si, la));
+    sm.split_b[tid] = static_cast<uint32_t>(min<size_t>(sj, lb));
+    if (tid == 0) {
+      sm.split_a[THREADS] = la;
+      sm.split_b[THREADS] = lb;
+    }
+  }
+  __syncthreads();
+
+  // Serial operation over this thread's A and B ranges.
+  uint32_t ia = sm.split_a[tid], ib = sm.split_b[tid];
+  const uint32_t ea = max(ia, sm.split_a[tid + 1]), eb = max(ib, sm.split_b[tid + 1]);
+  K outk[ITEMS];
+  uint32_t src[PAIRS ? ITEMS : 1];
+  uint32_t mask = 0;
+#pragma unroll
+  for (int k = 0; k < ITEMS; ++k) {
+    const bool a_ok = ia < ea, b_ok = ib < eb;
+    const K ka = sm.keys[min(ia, len ? len - 1 : 0u)];
+    const K kb = sm.keys[min(la + ib, len ? len - 1 : 0u)];
+    bool emit, emit_b, adv_a, adv_b;
+    serial_step<OP, K>(ka, kb, a_ok, b_ok, less, emit, emit_b, adv_a, adv_b);
+    outk[k] = emit_b ? kb : ka;
+    if constexpr (PAIRS) src[k] = emit_b ? la + ib : ia;
+    mask |= emit ? (1u << k) : 0u;
+    ia += adv_a ? 1u : 0u;
+    ib += adv_b ? 1u : 0u;
+  }
+  const uint32_t mine = __popc(mask);
+  V outv_reg[PAIRS ? ITEMS : 1];
+  if constexpr (PAIRS) {
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) outv_reg[k] = sm.vals[min(src[k], len ? len - 1 : 0u)];
+  }
+
+  // Block-wide exclusive scan of the emitted counts.
+  const uint32_t inc = wave_inclusive_sum(mine, lane);
+  if (lane == 63) sm.wave_total[wave] = inc;
+  __syncthreads();
+  uint32_t excl = inc - mine;
+  uint32_t tile_count = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    if (uint32_t(w) < wave) excl += sm.wave_total[w];
+    tile_count += sm.wave_total[w];
+  }
+
+  // Two-level decoupled look-back for the tile's output offset (wave 0).
+  if (wave == 0) {
+    const size_t g = t / GROUP;
+    const size_t gfirst = g * GROUP;
+    const uint32_t pos = static_cast<uint32_t>(t - gfirst);
+    if (lane == 0) {
+      store_agent(&desc[t], (t == 0 ? F_INCL : F_AGG) | uint64_t(tile_count));
+      add_agent(&gagg[g], uint64_t((1ull << GA_SHIFT) | tile_count));
+    }
+    uint64_t prefix = 0;
+    if (t > 0) {
+      bool done = false;
+      if (pos > 0) {
+        // In-group predecessors: lane l polls tile gfirst + l (l < pos) until
+        // every one has published; the sum then runs from the newest
+        // inclusive prefix (if any) up to this tile.
+        uint64_t d;
+        while (true) {
+          d = lane < pos ? load_agent(&desc[gfirst + lane]) : F_AGG;
+          if (__ballot((d >> 62) == 0) == 0) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+        const uint64_t incl = __ballot(lane < pos && (d >> 62) == 2);
+        const int hi = incl ? 63 - __clzll(static_cast<long long>(incl)) : -1;
+        prefix = wave_sum_u64((lane < pos && int(lane) >= hi) ? (d & VMASK) : 0);
+        done = hi >= 0;
+      }
+      // Earlier groups, newest first, 64 at a time: complete aggregates are
+      // summed until a group's inclusive prefix (groups before the first are
+      // read as an inclusive zero).
+      long long gg = static_cast<long long>(g) - 1;
+      while (!done) {
+        const long long gi = gg - static_cast<long long>(lane);
+        const uint64_t inc_w = gi >= 0 ? load_agent(&ginc[gi]) : F_INCL;
+        const uint64_t agg_w = gi >= 0 ? load_agent(&gagg[gi]) : 0;
+        const uint64_t incl_lanes = __ballot((inc_w >> 62) == 2);
+        const uint64_t full_lanes = __ballot((agg_w >> GA_SHIFT) == uint64_t(GROUP));
+        // First lane (newest group) holding an inclusive prefix, if any.
+        const int first_incl = incl_lanes ? __ffsll(static_cast<long long>(incl_lanes)) - 1 : 64;
+        // Groups before it must all be complete to be summed.
+        const uint64_t before = first_incl == 64 ? ~0ull : ((1ull << first_incl) - 1);
+        const int first_gap = (~full_lanes & before) ? __ffsll(static_cast<long long>(~full_lanes & before)) - 1 : 64;
+        if (first_gap < first_incl) {
+          // Sum the complete groups before the gap and poll again from it.
+          prefix += wave_sum_u64(int(lane) < first_gap ? (agg_w & GA_MASK) : 0);
+          gg -= first_gap;
+          if (first_gap == 0) __builtin_amdgcn_s_sleep(1);
+          continue;
+        }
+        uint64_t v = int(lane) < first_incl ? (agg_w & GA_MASK) : 0;
+        if (int(lane) == first_incl) v = inc_w & VMASK;
+        prefix += wave_sum_u64(v);
+        if (first_incl < 64) break;
+        gg -= 64;
+      }
+      if (lane == 0) store_agent(&desc[t], F_INCL | (prefix + tile_count));
+    }
+    const size_t glast = std::min(gfirst + GROUP, tiles) - 1;
+    if (lane == 0) {
+      if (t == glast) store_agent(&ginc[g], F_INCL | (prefix + tile_count));
+      if (t + 1 == tiles && out_count) *out_count = prefix + tile_count;
+      sm.tile_offset = prefix;
+    }
+  }
+  __syncthreads();
+  if (out == nullptr) return;  // count only
+
+  // Compact through LDS, then coalesced stores; positions at or past the
+  // destination's capacity are counted but not written.
+  const size_t base = sm.tile_offset;
+  if (base >= out_cap) return;  // uniform: the whole tile lies past the end
+  const uint32_t keep = static_cast<uint32_t>(std::min<size_t>(tile_count, out_cap - base));
+  __syncthreads();
+  {
+    uint32_t o = excl;
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+      if (mask & (1u << k)) {
+        sm.keys[o] = outk[k];
+        if constexpr (PAIRS) sm.vals[o] = outv_reg[k];
+        ++o;
+      }
+    }
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < keep; i += THREADS) {
+    out[base + i] = sm.keys[i];
+    if constexpr (PAIRS) outv[base + i] = sm.vals[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+struct SetArgs {
+  int op;
+  const void *a, *av, *b, *bv;
+  size_t na, nb;
+  void *out, *outv;
+  size_t out_cap;
+  uint64_t *out_count;
+  void *ws;
+  size_t ws_bytes;
+  hipStream_t stream;
+};
+
+struct Layout {
+  size_t tiles = 0, groups = 0;
+  size_t splits = 0, desc = 0, gagg = 0, ginc = 0, total = 0;
+};
+
+template <class K, class V>
+Layout layout(size_t na, size_t nb) {
+  Layout l;
+  const size_t total = na + nb;
+  constexpr size_t TILE = tile_items<K, V>();
+  l.tiles = total ? (total + TILE - 1) / TILE : 1;  // an empty input still reports its count
+  l.groups = (l.tiles + GROUP - 1) / GROUP;
+  size_t off = 0;
+  l.splits = off;
+  off += align_up((l.tiles + 1) * 2 * sizeof(uint64_t), 256);
+  l.desc = off;
+  off += l.tiles * sizeof(uint64_t);
+  l.gagg = off;
+  off += l.groups * sizeof(uint64_t);
+  l.ginc = off;
+  off += l.groups * sizeof(uint64_t);
+  l.total = align_up(off, 256);
+  return l;
+}
+
+template <class K, class V, class Cmp, int OP>
+rccl_hip_status run_op(const SetArgs &s) {
+  constexpr int ITEMS = items_for<K, V>();
+  constexpr size_t TILE = tile_items<K, V>();
+  const Layout l = layout<K, V>(s.na, s.nb);
+  if (!s.ws || s.ws_bytes < l.total)
+    return set_error(RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL, "set operation workspace", l.total,
+                     s.ws_bytes);
+  unsigned char *ws = static_cast<unsigned char *>(s.ws);
+  uint64_t *splits = reinterpret_cast<uint64_t *>(ws + l.splits);
+  uint64_t *desc = reinterpret_cast<uint64_t *>(ws + l.desc);
+  uint64_t *gagg = reinterpret_cast<uint64_t *>(ws + l.gagg);
+  uint64_t *ginc = reinterpret_cast<uint64_t *>(ws + l.ginc);
+  const size_t state_words = l.tiles + 2 * l.groups;
+  {
+    KernelTimer t("set_clear", s.stream, state_words);
+    clear_kernel<<<dim3(static_cast<uint32_t>(std::min<size_t>((state_words + 255) / 256, 1024))),
+                   256, 0, s.stream>>>(desc, state_words);
+  }
+  RCCL_HIP_TRY(check_launch("set clear"));
+  {
+    KernelTimer t("set_partition", s.stream, l.tiles + 1);
+    partition_kernel<K, Cmp><<<dim3(static_cast<uint32_t>((l.tiles + 1 + 255) / 256)), 256, 0,
+                               s.stream>>>(static_cast<const K *>(s.a), s.na,
+                                           static_cast<const K *>(s.b), s.nb, TILE, l.tiles + 1,
+                                           splits);
+  }
+  RCCL_HIP_TRY(check_launch("set partition"));
+  {
+    KernelTimer t("set_tile", s.stream, s.na + s.nb);
+    tile_kernel<K, V, Cmp, OP, ITEMS><<<dim3(static_cast<uint32_t>(l.tiles)), THREADS, 0,
+                                        s.stream>>>(
+        static_cast<const K *>(s.a), static_cast<const V *>(s.av), static_cast<const K *>(s.b),
+        static_cast<const V *>(s.bv), splits, l.tiles, static_cast<K *>(s.out),
+        static_cast<V *>(s.outv), s.out_cap, s.out_count, desc, gagg, ginc);
+  }
+  return check_launch("set tile");
+}
+
+template <class K, bool DESC>
+struct KindRunner {
+  template <class V>
+  static rccl_hip_status run(const SetArgs &s) {
+    using Cmp = ordering::Less<K, DESC>;
+    switch (s.op) {
+    case UNION: return run_op<K, V, Cmp, UNION>(s);
+    case INTERSECTION: return run_op<K, V, Cmp, INTERSECTION>(s);
+    case DIFFERENCE: return run_op<K, V, Cmp, DIFFERENCE>(s);
+    default: return run_op<K, V, Cmp, SYMMETRIC_DIFFERENCE>(s);
+    }
+  }
+};
+
+#define RCCL_SET_DECLARE_KIND(NAME)                                                       \
+  rccl_hip_status run_##NAME(const SetArgs &s, size_t value_bytes, bool descending);      \
+  size_t bytes_##NAME(size_t na, size_t nb, size_t value_bytes);
+RCCL_SET_DECLARE_KIND(u8)
+RCCL_SET_DECLARE_KIND(i8)
+RCCL_SET_DECLARE_KIND(u16)
+RCCL_SET_DECLARE_KIND(i16)
+RCCL_SET_DECLARE_KIND(u32)
+RCCL_SET_DECLARE_KIND(i32)
+RCCL_SET_DECLARE_KIND(f32)
+RCCL_SET_DECLARE_KIND(u64)
+RCCL_SET_DECLARE_KIND(i64)
+RCCL_SET_DECLARE_KIND(f64)
+#undef RCCL_SET_DECLARE_KIND
+
+#define RCCL_SET_DEFINE_KIND(NAME, KT)                                                      \
+  rccl_hip_status run_##NAME(const SetArgs &s, size_t value_bytes, bool descending) {       \
+    using Desc = KindRunner<KT, true>;                                                      \
+    using Asc = KindRunner<KT, false>;                                                      \
+    if (descending) {                                                                       \
+      RCCL_ORDERING_DISPATCH_VALUE(value_bytes, Desc, s)                                    \
+    } else {                                                                                \
+      RCCL_ORDERING_DISPATCH_VALUE(value_bytes, Asc, s)                                     \
+    }                                                                                       \
+    return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "set operation value bytes");         \
+  }                                                                                         \
+  size_t bytes_##NAME(size_t na, size_t nb, size_t value_bytes) {                           \
+    switch (value_bytes) {                                                                  \
+    case 0: return layout<KT, ordering::NoValue>(na, nb).total;                             \
+    case 1: return layout<KT, uint8_t>(na, nb).total;                                       \
+    case 2: return layout<KT, uint16_t>(na, nb).total;                                      \
+    case 4: return layout<KT, uint32_t>(na, nb).total;                                      \
+    case 8: return layout<KT, uint64_t>(na, nb).total;                                      \
+    default: return layout<KT, Value16>(na, nb).total;                                      \
+    }                                                                                       \
+  }
+
+} // namespace set_ops
+} // namespace rccl_hip

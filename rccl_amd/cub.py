@@ -6,6 +6,8 @@ the StarGazerM/rccl tree):
   device_radix_sort_*                  rccl-cub/src/dispatch.rs:2091-2943
   device_merge_{keys,pairs}            rccl-cub/src/dispatch.rs:1572,1915
   device_merge_sort_*                  rccl-cub/src/dispatch.rs:170-322,1116-1400
+  device_set_{keys,pairs}              rccl-cub/src/set_operation.rs:265-589 (the
+                                       four operations; output=None counts only)
   typed workspaces                     rccl-cub/src/workspace.rs:108-706
   DoubleBuffer                         rccl-cub/src/double_buffer.rs:6-130
 All calls are stream-ordered and asynchronous, as in CUB; every argument is
@@ -244,3 +246,199 @@ def device_radix_sort_pairs_buffer(launch, buffers, bit_range, workspace):
 
 def device_radix_sort_pairs_buffer_descending(launch, buffers, bit_range, workspace):
     _radix_buffer(launch, buffers, bit_range, workspace, DESCENDING, True)
+
+
+# ---------------------------------------------------------------------------
+# DeviceMerge (rccl-cub/src/merge.rs:194-368, dispatch.rs:1572,1915).
+# ---------------------------------------------------------------------------
+def _ordering_kind(dtype) -> str:
+    kind = kind_of(dtype)
+    if kind not in _abi.KEY_KINDS:
+        raise TypeError(f"{dtype} has no prebuilt ordering kernels")
+    return kind
+
+
+def _value_bytes(value_dtype) -> int:
+    return 0 if value_dtype is None else np.dtype(value_dtype).itemsize
+
+
+class DeviceMergeWorkspace:
+    """Caller-owned partition storage for one merge shape."""
+
+    def __init__(self, launch: Launch, key_dtype, na: int, nb: int, value_dtype=None):
+        self.key_kind = _ordering_kind(key_dtype)
+        self.value_bytes = _value_bytes(value_dtype)
+        self.na, self.nb = na, nb
+        self.control_bytes = _abi.workspace_bytes(
+            "rccl_hip_merge_workspace_bytes", _abi.KEY_KINDS[self.key_kind], self.value_bytes,
+            na, nb)
+        self.control = DeviceBuffer.bytes(self.control_bytes, launch.program.device)
+
+
+def device_merge_workspace(launch, key_dtype, na, nb):
+    return DeviceMergeWorkspace(launch, key_dtype, na, nb)
+
+
+def device_merge_pairs_workspace(launch, key_dtype, value_dtype, na, nb):
+    return DeviceMergeWorkspace(launch, key_dtype, na, nb, value_dtype)
+
+
+def _ws_ptr(ws):
+    return (ws.control.ptr if ws.control_bytes else None), ws.control_bytes
+
+
+def device_merge_keys(launch, first, second, workspace, output, order=ascending):
+    """Stable merge of two sorted ranges; equal keys take `first` first."""
+    total = first.len() + second.len()
+    _check_len("output", total, output.len())
+    kind = _ordering_kind(first.dtype)
+    wptr, wbytes = _ws_ptr(workspace)
+    _abi.check(_abi.load().rccl_hip_merge(
+        _abi.KEY_KINDS[kind], 0, order_code(order), first.ptr, None, first.len(), second.ptr,
+        None, second.len(), output.ptr, None, wptr, wbytes, launch.handle))
+
+
+def device_merge_pairs(launch, first_keys, first_values, second_keys, second_values, workspace,
+                       output_keys, output_values, order=ascending):
+    _check_len("first values", first_keys.len(), first_values.len())
+    _check_len("second values", second_keys.len(), second_values.len())
+    total = first_keys.len() + second_keys.len()
+    _check_len("output keys", total, output_keys.len())
+    _check_len("output values", total, output_values.len())
+    kind = _ordering_kind(first_keys.dtype)
+    wptr, wbytes = _ws_ptr(workspace)
+    _abi.check(_abi.load().rccl_hip_merge(
+        _abi.KEY_KINDS[kind], first_values.dtype.itemsize, order_code(order), first_keys.ptr,
+        first_values.ptr, first_keys.len(), second_keys.ptr, second_values.ptr,
+        second_keys.len(), output_keys.ptr, output_values.ptr, wptr, wbytes, launch.handle))
+
+
+# ---------------------------------------------------------------------------
+# DeviceMergeSort (rccl-cub/src/merge_sort.rs:140-690, dispatch.rs:170-322,1116-1400).
+# ---------------------------------------------------------------------------
+class DeviceMergeSortWorkspace:
+    """Caller-owned scratch keys/values and partitions for one sort length."""
+
+    def __init__(self, launch: Launch, key_dtype, n: int, value_dtype=None):
+        self.key_kind = _ordering_kind(key_dtype)
+        self.value_bytes = _value_bytes(value_dtype)
+        self.n = n
+        self.control_bytes = _abi.workspace_bytes(
+            "rccl_hip_merge_sort_workspace_bytes", _abi.KEY_KINDS[self.key_kind],
+            self.value_bytes, n)
+        self.control = DeviceBuffer.bytes(self.control_bytes, launch.program.device)
+
+
+def device_merge_sort_workspace(launch, key_dtype, n):
+    return DeviceMergeSortWorkspace(launch, key_dtype, n)
+
+
+def device_merge_sort_pairs_workspace(launch, key_dtype, value_dtype, n):
+    return DeviceMergeSortWorkspace(launch, key_dtype, n, value_dtype)
+
+
+def _merge_sort(launch, in_keys, in_values, out_keys, out_values, ws, order):
+    n = in_keys.len()
+    _check_len("merge-sort workspace", ws.n, n)
+    kind = _ordering_kind(in_keys.dtype)
+    vb = 0 if in_values is None else in_values.dtype.itemsize
+    wptr, wbytes = _ws_ptr(ws)
+    _abi.check(_abi.load().rccl_hip_merge_sort(
+        _abi.KEY_KINDS[kind], vb, order_code(order), in_keys.ptr,
+        None if in_values is None else in_values.ptr, out_keys.ptr,
+        None if out_values is None else out_values.ptr, n, wptr, wbytes, launch.handle))
+
+
+def device_merge_sort_keys(launch, keys, workspace, order=ascending):
+    """Stable in-place merge sort of `keys`."""
+    _merge_sort(launch, keys, None, keys, None, workspace, order)
+
+
+def device_merge_sort_keys_copy(launch, input, workspace, output, order=ascending):
+    _check_len("output keys", input.len(), output.len())
+    _merge_sort(launch, input, None, output, None, workspace, order)
+
+
+def device_merge_sort_pairs(launch, keys, values, workspace, order=ascending):
+    _check_len("values", keys.len(), values.len())
+    _merge_sort(launch, keys, values, keys, values, workspace, order)
+
+
+def device_merge_sort_pairs_copy(launch, input_keys, input_values, workspace, output_keys,
+                                 output_values, order=ascending):
+    n = input_keys.len()
+    _check_len("input values", n, input_values.len())
+    _check_len("output keys", n, output_keys.len())
+    _check_len("output values", n, output_values.len())
+    _merge_sort(launch, input_keys, input_values, output_keys, output_values, workspace, order)
+
+
+# ---------------------------------------------------------------------------
+# Set operations (rccl-cub/src/set_operation.rs:265-589, dispatch.rs:344-1000).
+# ---------------------------------------------------------------------------
+SET_OPERATIONS = _abi.SET_OPS
+
+
+def set_output_capacity(operation, na: int, nb: int) -> int:
+    """Largest possible output of a set operation over na + nb keys."""
+    op = SET_OPERATIONS[operation] if isinstance(operation, str) else operation
+    return {0: na + nb, 1: min(na, nb), 2: na, 3: na + nb}[op]
+
+
+class DeviceSetOperationWorkspace:
+    """Caller-owned tile state, partitions and the device output count."""
+
+    def __init__(self, launch: Launch, operation: str, key_dtype, na: int, nb: int,
+                 value_dtype=None):
+        self.operation = SET_OPERATIONS[operation]
+        self.key_kind = _ordering_kind(key_dtype)
+        self.value_bytes = _value_bytes(value_dtype)
+        self.control_bytes = _abi.workspace_bytes(
+            "rccl_hip_set_op_workspace_bytes", self.operation, _abi.KEY_KINDS[self.key_kind],
+            self.value_bytes, na, nb)
+        self.control = DeviceBuffer.bytes(self.control_bytes, launch.program.device)
+        self.output_count = DeviceBuffer.zeroed(np.dtype(np.uint64), 1, launch.program.device)
+
+    def count(self) -> int:
+        """Read the last operation's output length (synchronizes)."""
+        return int(self.output_count.to_host_vec()[0])
+
+
+def device_set_workspace(launch, operation, key_dtype, na, nb):
+    return DeviceSetOperationWorkspace(launch, operation, key_dtype, na, nb)
+
+
+def device_set_pairs_workspace(launch, operation, key_dtype, value_dtype, na, nb):
+    return DeviceSetOperationWorkspace(launch, operation, key_dtype, na, nb, value_dtype)
+
+
+def _set_op(launch, op, first_keys, first_values, second_keys, second_values, ws, output_keys,
+            output_values, order):
+    kind = _ordering_kind(first_keys.dtype)
+    vb = 0
+    if output_keys is not None and first_values is not None:
+        _check_len("first set values", first_keys.len(), first_values.len())
+        if op in (0, 3):
+            _check_len("second set values", second_keys.len(), second_values.len())
+        _check_len("set output values", output_keys.len(), output_values.len())
+        vb = first_values.dtype.itemsize
+    _abi.check(_abi.load().rccl_hip_set_op(
+        op, _abi.KEY_KINDS[kind], vb, order_code(order), first_keys.ptr,
+        None if first_values is None else first_values.ptr, first_keys.len(), second_keys.ptr,
+        None if second_values is None else second_values.ptr, second_keys.len(),
+        None if output_keys is None else output_keys.ptr,
+        None if output_values is None or vb == 0 else output_values.ptr,
+        0 if output_keys is None else output_keys.len(), ws.output_count.ptr, ws.control.ptr, ws.control_bytes, launch.handle))
+
+
+def device_set_keys(launch, operation, first, second, workspace, output=None, order=ascending):
+    """Enqueue a keys-only set operation; `output=None` only counts. The
+    length lands in `workspace.output_count` (device)."""
+    _set_op(launch, SET_OPERATIONS[operation], first, None, second, None, workspace, output,
+            None, order)
+
+
+def device_set_pairs(launch, operation, first_keys, first_values, second_keys, second_values,
+                     workspace, output_keys, output_values, order=ascending):
+    _set_op(launch, SET_OPERATIONS[operation], first_keys, first_values, second_keys,
+            second_values, workspace, output_keys, output_values, order)

@@ -1,0 +1,272 @@
+"""Python mirror of the reference's rccl-thrust ordering facade over the C ABI.
+
+Names, routing and error behaviour follow rccl-thrust (paths relative to the
+StarGazerM/rccl tree):
+  Program.load / Program.par           rccl-thrust/src/cuda.rs:85-109
+  sort, sort_unstable (natural order)  ordering.rs:13-44  -> radix sort, ascending
+  sort_by, sort_unstable_by (closure)  ordering.rs:13-44  -> stable merge sort
+  view().with_values(..)               range.rs:100-163, ordering.rs:96-129
+  a.merge(b).write_into(out, exec)     merge.rs:16-247
+  a.union(b).write_into / .count       set.rs:357-898 (also intersection,
+                                       difference, symmetric_difference)
+Every call allocates its temporary workspace on the device, runs on the
+execution's stream and synchronizes before returning, as Thrust's
+synchronous policy does (rccl-thrust/src/backend.rs:8-150).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import cub
+from ._abi import DeviceAlgorithmError  # noqa: F401  (re-export)
+from .device import DeviceBuffer
+
+ascending = cub.ascending
+descending = cub.descending
+
+
+class Program:
+    """Loaded kernel program for one device."""
+
+    def __init__(self, inner: cub.Program):
+        self._inner = inner
+
+    @staticmethod
+    def load(device: int = 0) -> "Program":
+        return Program(cub.Program.load(device))
+
+    @property
+    def device(self) -> int:
+        return self._inner.device
+
+    def par(self, stream: torch.cuda.Stream | None = None) -> "Execution":
+        return Execution(self._inner.on(stream))
+
+
+class Execution:
+    """A synchronous execution policy bound to one stream."""
+
+    def __init__(self, launch: cub.Launch):
+        self._launch = launch
+
+    def launch(self) -> cub.Launch:
+        return self._launch
+
+    def synchronize(self) -> None:
+        self._launch.synchronize()
+
+
+# ---------------------------------------------------------------------------
+# Views.
+# ---------------------------------------------------------------------------
+class DeviceView:
+    def __init__(self, buffer: DeviceBuffer):
+        self.buffer = buffer
+
+    def len(self) -> int:
+        return self.buffer.len()
+
+    def with_values(self, values: "DeviceView | DeviceBuffer") -> "KeyValueRange":
+        values = values if isinstance(values, DeviceView) else DeviceView(values)
+        if values.len() != self.len():
+            cub._check_len("values", self.len(), values.len())
+        return KeyValueRange(self, values)
+
+    def merge(self, second: "DeviceView") -> "_Merge":
+        return _Merge(self, second, ascending)
+
+    def merge_by(self, second: "DeviceView", order) -> "_Merge":
+        return _Merge(self, second, order)
+
+    def union(self, second):
+        return _SetExpression("union", self, second, ascending)
+
+    def union_by(self, second, order):
+        return _SetExpression("union", self, second, order)
+
+    def intersection(self, second):
+        return _SetExpression("intersection", self, second, ascending)
+
+    def intersection_by(self, second, order):
+        return _SetExpression("intersection", self, second, order)
+
+    def difference(self, second):
+        return _SetExpression("difference", self, second, ascending)
+
+    def difference_by(self, second, order):
+        return _SetExpression("difference", self, second, order)
+
+    def symmetric_difference(self, second):
+        return _SetExpression("symmetric_difference", self, second, ascending)
+
+    def symmetric_difference_by(self, second, order):
+        return _SetExpression("symmetric_difference", self, second, order)
+
+
+class DeviceViewMut(DeviceView):
+    def as_view(self) -> DeviceView:
+        return DeviceView(self.buffer)
+
+    def with_values(self, values) -> "KeyValueRangeMut":
+        values = values if isinstance(values, DeviceView) else DeviceView(values)
+        if values.len() != self.len():
+            cub._check_len("values", self.len(), values.len())
+        return KeyValueRangeMut(self, values)
+
+
+class KeyValueRange:
+    """Structure-of-arrays keys plus values; orderings examine keys only."""
+
+    def __init__(self, keys: DeviceView, values: DeviceView):
+        self.keys = keys
+        self.values = values
+
+    def len(self) -> int:
+        return self.keys.len()
+
+    def merge(self, second: "KeyValueRange") -> "_Merge":
+        return _Merge(self, second, ascending)
+
+    def merge_by(self, second: "KeyValueRange", order) -> "_Merge":
+        return _Merge(self, second, order)
+
+    def union(self, second):
+        return _SetExpression("union", self, second, ascending)
+
+    def union_by(self, second, order):
+        return _SetExpression("union", self, second, order)
+
+    def intersection(self, second):
+        return _SetExpression("intersection", self, second, ascending)
+
+    def intersection_by(self, second, order):
+        return _SetExpression("intersection", self, second, order)
+
+    def difference(self, second):
+        return _SetExpression("difference", self, second, ascending)
+
+    def difference_by(self, second, order):
+        return _SetExpression("difference", self, second, order)
+
+    def symmetric_difference(self, second):
+        return _SetExpression("symmetric_difference", self, second, ascending)
+
+    def symmetric_difference_by(self, second, order):
+        return _SetExpression("symmetric_difference", self, second, order)
+
+
+class KeyValueRangeMut(KeyValueRange):
+    pass
+
+
+def view(buffer: DeviceBuffer) -> DeviceView:
+    return DeviceView(buffer)
+
+
+def view_mut(buffer: DeviceBuffer) -> DeviceViewMut:
+    return DeviceViewMut(buffer)
+
+
+# ---------------------------------------------------------------------------
+# Sorting (rccl-thrust/src/ordering.rs, backend.rs).
+# ---------------------------------------------------------------------------
+def _split(target):
+    if isinstance(target, KeyValueRange):
+        return target.keys.buffer, target.values.buffer
+    if isinstance(target, DeviceView):
+        return target.buffer, None
+    return target, None
+
+
+def _radix(execution: Execution, target) -> None:
+    keys, values = _split(target)
+    launch = execution.launch()
+    if values is None:
+        ws = cub.device_radix_sort_workspace(launch, keys.dtype, keys.len())
+        cub.device_radix_sort_keys(launch, keys, ws)
+    else:
+        ws = cub.device_radix_sort_pairs_workspace(launch, keys.dtype, values.dtype, keys.len())
+        cub.device_radix_sort_pairs(launch, keys, values, ws)
+    execution.synchronize()
+
+
+def _merge_sort(execution: Execution, target, order) -> None:
+    keys, values = _split(target)
+    launch = execution.launch()
+    if values is None:
+        ws = cub.device_merge_sort_workspace(launch, keys.dtype, keys.len())
+        cub.device_merge_sort_keys(launch, keys, ws, order)
+    else:
+        ws = cub.device_merge_sort_pairs_workspace(launch, keys.dtype, values.dtype, keys.len())
+        cub.device_merge_sort_pairs(launch, keys, values, ws, order)
+    execution.synchronize()
+
+
+def sort_unstable(target, execution: Execution) -> None:
+    """Natural-order sort (radix, ascending)."""
+    _radix(execution, target)
+
+
+def sort(target, execution: Execution) -> None:
+    """Stable natural-order sort (radix sort is stable)."""
+    _radix(execution, target)
+
+
+def sort_unstable_by(target, execution: Execution, order) -> None:
+    """Sort by a comparator (stable merge sort)."""
+    _merge_sort(execution, target, order)
+
+
+def sort_by(target, execution: Execution, order) -> None:
+    """Stable sort by a comparator (merge sort)."""
+    _merge_sort(execution, target, order)
+
+
+# ---------------------------------------------------------------------------
+# Merge and set expressions (rccl-thrust/src/merge.rs, set.rs).
+# ---------------------------------------------------------------------------
+class _Merge:
+    def __init__(self, first, second, order):
+        self.first, self.second, self.order = first, second, order
+
+    def write_into(self, output, execution: Execution) -> None:
+        launch = execution.launch()
+        ak, av = _split(self.first)
+        bk, bv = _split(self.second)
+        ok, ov = _split(output)
+        if av is None:
+            ws = cub.device_merge_workspace(launch, ak.dtype, ak.len(), bk.len())
+            cub.device_merge_keys(launch, ak, bk, ws, ok, self.order)
+        else:
+            ws = cub.device_merge_pairs_workspace(launch, ak.dtype, av.dtype, ak.len(), bk.len())
+            cub.device_merge_pairs(launch, ak, av, bk, bv, ws, ok, ov, self.order)
+        execution.synchronize()
+
+
+class _SetExpression:
+    def __init__(self, operation, first, second, order):
+        self.operation, self.first, self.second, self.order = operation, first, second, order
+
+    def _run(self, output, execution: Execution) -> int:
+        launch = execution.launch()
+        ak, av = _split(self.first)
+        bk, bv = _split(self.second)
+        ok, ov = (None, None) if output is None else _split(output)
+        if ak.len() + bk.len() == 0:
+            return 0  # rccl-thrust/src/set.rs:44-46: empty inputs return 0 without launching
+        if av is None or ok is None:
+            ws = cub.device_set_workspace(launch, self.operation, ak.dtype, ak.len(), bk.len())
+            cub.device_set_keys(launch, self.operation, ak, bk, ws, ok, self.order)
+        else:
+            ws = cub.device_set_pairs_workspace(launch, self.operation, ak.dtype, av.dtype,
+                                                ak.len(), bk.len())
+            cub.device_set_pairs(launch, self.operation, ak, av, bk, bv, ws, ok, ov, self.order)
+        return ws.count()  # reads the device count back (synchronizes)
+
+    def write_into(self, output, execution: Execution) -> int:
+        """Write the result and return its length."""
+        return self._run(output, execution)
+
+    def count(self, execution: Execution) -> int:
+        """Execute the operation without materializing its keys."""
+        return self._run(None, execution)

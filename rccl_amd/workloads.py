@@ -32,20 +32,37 @@ _CHUNK = 1 << 24
 
 def splitmix64(x: np.ndarray) -> np.ndarray:
     """splitmix64 finaliser applied elementwise to uint64 states."""
-    x = np.asarray(x, dtype=_U64) + _U64(0x9E3779B97F4A7C15)
-    x = (x ^ (x >> _U64(30))) * _U64(0xBF58476D1CE4E5B9)
-    x = (x ^ (x >> _U64(27))) * _U64(0x94D049BB133111EB)
-    return x ^ (x >> _U64(31))
+    out = np.array(x, dtype=_U64, copy=True)
+    _splitmix64_inplace(out, np.empty_like(out))
+    return out
+
+
+def _splitmix64_inplace(x: np.ndarray, tmp: np.ndarray) -> None:
+    # In place over preallocated buffers: fresh temporaries per operation
+    # would cost more in first-touch page faults than the arithmetic.
+    with np.errstate(over="ignore"):
+        np.add(x, _U64(0x9E3779B97F4A7C15), out=x)
+        for shift, mult in ((30, 0xBF58476D1CE4E5B9), (27, 0x94D049BB133111EB)):
+            np.right_shift(x, _U64(shift), out=tmp)
+            np.bitwise_xor(x, tmp, out=x)
+            np.multiply(x, _U64(mult), out=x)
+        np.right_shift(x, _U64(31), out=tmp)
+        np.bitwise_xor(x, tmp, out=x)
 
 
 def hash_range(seed: int, n: int, start: int = 0) -> np.ndarray:
     """splitmix64(seed + i) for i in [start, start + n), as uint64."""
     out = np.empty(n, dtype=_U64)
+    if n == 0:
+        return out
+    base = np.arange(min(n, _CHUNK), dtype=_U64)
+    tmp = np.empty(min(n, _CHUNK), dtype=_U64)
     for lo in range(0, n, _CHUNK):
         hi = min(n, lo + _CHUNK)
-        idx = np.arange(start + lo, start + hi, dtype=_U64)
+        x = out[lo:hi]
         with np.errstate(over="ignore"):
-            out[lo:hi] = splitmix64(idx + _U64(seed))
+            np.add(base[:hi - lo], _U64((seed + start + lo) & 0xFFFFFFFFFFFFFFFF), out=x)
+        _splitmix64_inplace(x, tmp[:hi - lo])
     return out
 
 
@@ -148,7 +165,13 @@ def c3_keys(n: int = 1 << 28) -> np.ndarray:
 
 
 def _sorted_u32_24bit(n: int, seed: int) -> np.ndarray:
-    return np.sort((hash_range(seed, n) >> _U64(40)).astype(np.uint32), kind="stable")
+    """The n values (splitmix64(seed + i) >> 40) in ascending order, built by
+    counting (the values lie in [0, 2^24))."""
+    counts = np.zeros(1 << 24, dtype=np.int64)
+    for lo in range(0, n, _CHUNK):
+        part = (hash_range(seed, min(n, lo + _CHUNK) - lo, lo) >> _U64(40)).astype(np.int64)
+        counts += np.bincount(part, minlength=1 << 24)
+    return np.repeat(np.arange(1 << 24, dtype=np.uint32), counts)
 
 
 def c4_merge_inputs(n_each: int = 1 << 27):
