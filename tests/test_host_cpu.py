@@ -1,0 +1,161 @@
+"""CPU tests of the host side: the C ABI library loads and exports every
+symbol the header declares, validation rejects bad calls before any launch
+(no GPU needed), and the Python mirrors and workload generators behave as
+the reference's host code does."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from rccl_amd import _abi, cub, workloads
+from rccl_amd.device import KIND_DTYPES, kind_of
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rccl_hip.h")
+FAKE = ctypes.c_void_p(4096)  # never dereferenced: every call below fails validation first
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _abi.load()
+
+
+def _declared():
+    text = open(HEADER).read()
+    return re.findall(r"RCCL_HIP_API\s+[^;]*?\b(rccl_hip_\w+)\s*\(", text)
+
+
+def test_header_symbols_exported(lib):
+    names = _declared()
+    assert len(names) >= 15
+    out = subprocess.run(["nm", "-D", "--defined-only", _abi.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    # Nothing beyond the declared C ABI leaks out of the library.
+    extra = sorted(n for n in exported if n.startswith("rccl_hip") and n not in names)
+    assert not extra, extra
+    assert set(_abi.EXPORTED_SYMBOLS) <= set(names)
+
+
+def test_status_strings_and_version(lib):
+    assert lib.rccl_hip_abi_version() >= 1
+    lib.rccl_hip_status_string.restype = ctypes.c_char_p
+    assert lib.rccl_hip_status_string(0) == b"success"
+    assert b"workspace" in lib.rccl_hip_status_string(2)
+    assert b"bit range" in lib.rccl_hip_status_string(3)
+
+
+def _last():
+    info = _abi.ErrorInfo()
+    _abi.load().rccl_hip_last_error(ctypes.byref(info))
+    return info
+
+
+def test_radix_validation_before_launch(lib):
+    cur = ctypes.c_int(1)
+    # Reversed and out-of-key bit windows (rccl-cub/src/radix.rs:364-392).
+    for begin, end in [(5, 4), (0, 33), (40, 48)]:
+        rc = lib.rccl_hip_radix_sort_buffer(0, 0, 0, FAKE, FAKE, None, None, 100,
+                                            ctypes.byref(cur), begin, end, FAKE, 1 << 20, None)
+        assert rc == 3
+        info = _last()
+        assert (info.begin_bit, info.end_bit, info.key_bits) == (begin, end, 32)
+    # A workspace smaller than required reports both sizes.
+    need = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", 0, 0, 1000)
+    rc = lib.rccl_hip_radix_sort_buffer(0, 0, 0, FAKE, FAKE, None, None, 1000, ctypes.byref(cur),
+                                        0, 32, FAKE, need - 1, None)
+    assert rc == 2
+    info = _last()
+    assert (info.expected, info.actual) == (need, need - 1)
+    # Unsupported key kinds and value widths.
+    out = ctypes.c_size_t()
+    assert lib.rccl_hip_radix_sort_workspace_bytes(6, 0, 10, ctypes.byref(out)) == 9  # u8
+    assert lib.rccl_hip_radix_sort_workspace_bytes(0, 3, 10, ctypes.byref(out)) == 9
+
+
+def test_merge_and_sort_validation(lib):
+    huge = (1 << 64) - 1
+    assert lib.rccl_hip_merge(0, 0, 0, FAKE, None, huge, FAKE, None, 2, FAKE, None, FAKE, 1,
+                              None) == 5  # SizeOverflow
+    need = _abi.workspace_bytes("rccl_hip_merge_workspace_bytes", 0, 0, 50_000, 50_000)
+    assert lib.rccl_hip_merge(0, 0, 0, FAKE, None, 50_000, FAKE, None, 50_000, FAKE, None, FAKE,
+                              need - 1, None) == 2
+    assert lib.rccl_hip_merge(0, 4, 0, FAKE, None, 10, FAKE, None, 10, FAKE, None, FAKE,
+                              need, None) == 9  # values missing
+    assert lib.rccl_hip_merge(0, 0, 0, None, None, 0, None, None, 0, None, None, None, 0,
+                              None) == 0  # empty: nothing to do
+    need = _abi.workspace_bytes("rccl_hip_merge_sort_workspace_bytes", 3, 8, 100_000)
+    assert lib.rccl_hip_merge_sort(3, 8, 0, FAKE, FAKE, FAKE, FAKE, 100_000, FAKE, need - 1,
+                                   None) == 2
+    assert lib.rccl_hip_merge_sort(3, 8, 2, FAKE, FAKE, FAKE, FAKE, 10, FAKE, need, None) == 9
+
+
+def test_set_validation(lib):
+    assert lib.rccl_hip_set_op(9, 0, 0, 0, FAKE, None, 10, FAKE, None, 10, FAKE, None, 20, FAKE,
+                               FAKE, 1 << 20, None) == 9  # unknown operation
+    assert lib.rccl_hip_set_op(0, 0, 0, 0, FAKE, None, 10, FAKE, None, 10, None, None, 0, None,
+                               FAKE, 1 << 20, None) == 9  # count-only needs a count
+    need = _abi.workspace_bytes("rccl_hip_set_op_workspace_bytes", 0, 3, 0, 1 << 20, 1 << 20)
+    assert lib.rccl_hip_set_op(0, 3, 0, 0, FAKE, None, 1 << 20, FAKE, None, 1 << 20, FAKE, None,
+                               1 << 21, FAKE, FAKE, need - 1, None) == 2
+    # Union reads the second range's values; intersection does not.
+    assert lib.rccl_hip_set_op(0, 0, 4, 0, FAKE, FAKE, 10, FAKE, None, 10, FAKE, FAKE, 20, FAKE,
+                               FAKE, 1 << 20, None) == 9
+
+
+def test_workspace_sizes_scale(lib):
+    small = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", 0, 0, 1 << 10)
+    big = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", 0, 0, 1 << 28)
+    assert 0 < small < big < (1 << 28)  # control state only, well under the keys themselves
+    assert _abi.workspace_bytes("rccl_hip_merge_workspace_bytes", 0, 0, 0, 0) == 0
+    ms = _abi.workspace_bytes("rccl_hip_merge_sort_workspace_bytes", 0, 4, 1 << 20)
+    assert ms >= (1 << 20) * 8  # scratch keys and values
+
+
+def test_python_mirror_host_logic():
+    assert cub.order_code(None) == cub.ASCENDING
+    assert cub.order_code(cub.descending) == cub.DESCENDING
+    with pytest.raises(ValueError):
+        cub.order_code(lambda a, b: 0)
+    assert cub.ascending(1, 2) == -1 and cub.descending(1, 2) == 1
+    with pytest.raises(_abi.DeviceAlgorithmError) as e:
+        cub._check_len("output", 7, 6)
+    assert e.value.role == "output" and (e.value.expected, e.value.actual) == (7, 6)
+    assert cub.set_output_capacity("intersection", 5, 9) == 5
+    assert cub.set_output_capacity("difference", 5, 9) == 5
+    assert cub.set_output_capacity("union", 5, 9) == 14
+    for k, d in KIND_DTYPES.items():
+        assert kind_of(d) == k
+
+
+def test_workloads_deterministic_and_shaped():
+    assert int(workloads.splitmix64(np.array([0], np.uint64))[0]) == 0xE220A8397B1DCDAF
+    a = workloads.hash_range(123, 1000, 17)
+    b = workloads.hash_range(123, 1017)[17:]
+    assert np.array_equal(a, b)
+    k = workloads.c1_keys(1 << 12)
+    assert k.dtype == np.uint32 and np.array_equal(k, workloads.c1_keys(1 << 12))
+    ka, pa, kb, pb = workloads.c4_merge_inputs(1 << 12)
+    assert (np.diff(ka.astype(np.int64)) >= 0).all() and (np.diff(kb.astype(np.int64)) >= 0).all()
+    assert ka.max() < (1 << 24) and (pb >> 31).all() and not (pa >> 31).any()
+    x, y = workloads.c5_inputs(1 << 12)
+    assert x.size == y.size == 1 << 12 and x.dtype == np.uint64
+    assert (np.diff(x) >= 0).all() and (np.diff(y) >= 0).all()
+    c3 = workloads.c3_keys(1 << 14)
+    counts = workloads.c3_special_counts(1 << 14)
+    bits = c3.view(np.uint32)
+    assert int((bits == 0x80000000).sum()) >= counts["-0"]
+    assert int((bits == 0x7FC00000).sum()) == counts["nan"]
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=600)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)

@@ -1,0 +1,302 @@
+"""CPU checks that pin the oracle (oracle/oracle.c) before it is trusted.
+
+Each oracle function is checked against
+  * the literal vectors of the reference's own probes and tests
+    (tests/golden/reference_vectors.json, each case citing its source), and
+  * an independent restatement that shares no code with the oracle: numpy's
+    stable argsort over the order-preserving key transform for radix sort,
+    `heapq.merge` for merge, Python's stable `sorted` for merge sort, and
+    multiset (Counter) algebra plus a per-run value rule for the set
+    operations,
+chosen so that a plausible mistake (a tie broken the wrong way, a missing
+sign flip, a wrong ±0 rule, values taken from the wrong range) fails.
+"""
+import collections
+import heapq
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.json")
+NP = {"u8": np.uint8, "i8": np.int8, "u16": np.uint16, "i16": np.int16, "u32": np.uint32,
+      "i32": np.int32, "f32": np.float32, "u64": np.uint64, "i64": np.int64, "f64": np.float64}
+BITS_OF = {1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}
+OPS = ["union", "intersection", "difference", "symmetric_difference"]
+
+
+def _keys(case, field, kind):
+    vals = case[field]
+    if case.get("float_bits"):
+        bits = np.array([int(v, 16) for v in vals], dtype=BITS_OF[np.dtype(NP[kind]).itemsize])
+        return bits.view(NP[kind])
+    return np.array(vals, dtype=NP[kind])
+
+
+def _bits(a):
+    a = np.asarray(a)
+    return a.view(BITS_OF[a.dtype.itemsize])
+
+
+def _golden_cases():
+    with open(GOLDEN) as f:
+        return json.load(f)["cases"]
+
+
+@pytest.mark.parametrize("case", _golden_cases(), ids=lambda c: c["id"])
+def test_oracle_reproduces_reference_vectors(case):
+    kind, desc = case["kind"], case["descending"]
+    vdt = NP.get(case.get("value_dtype", ""), None)
+    if case["op"] == "radix_sort":
+        keys = _keys(case, "keys", kind)
+        vals = None if "values" not in case else np.array(case["values"], dtype=vdt)
+        out = oracle.radix_sort(kind, keys, vals, desc, case.get("begin_bit", 0),
+                                case.get("end_bit"))
+    elif case["op"] == "merge":
+        a, b = _keys(case, "a", kind), _keys(case, "b", kind)
+        if "a_values" in case:
+            out = oracle.merge(kind, a, b, np.array(case["a_values"], vdt),
+                               np.array(case["b_values"], vdt), desc)
+        else:
+            out = oracle.merge(kind, a, b, descending=desc)
+    elif case["op"] == "merge_sort":
+        keys = _keys(case, "keys", kind)
+        vals = None if "values" not in case else np.array(case["values"], dtype=vdt)
+        out = oracle.merge_sort(kind, keys, vals, desc)
+    else:
+        a, b = _keys(case, "a", kind), _keys(case, "b", kind)
+        av = None if "a_values" not in case else np.array(case["a_values"], vdt)
+        bv = None if "b_values" not in case else np.array(case["b_values"], vdt)
+        out = oracle.set_op(case["set_op"], kind, a, b, av, bv, desc)
+        assert oracle.set_op(case["set_op"], kind, a, b, descending=desc,
+                             count_only=True) == len(case["expected_keys"])
+    keys_out, vals_out = (out if isinstance(out, tuple) else (out, None))
+    assert np.array_equal(_bits(keys_out), _bits(_keys(case, "expected_keys", kind)))
+    if "expected_values" in case:
+        assert vals_out.tolist() == case["expected_values"]
+
+
+# ---------------------------------------------------------------------------
+# Radix sort vs an independent numpy restatement of the key transform
+# (rccl-cub/src/ordering_backend/radix.rs:75-337): unsigned identity, signed
+# sign flip, float `neg ? !raw : raw ^ sign`, descending = complement, and for
+# float digits the ordered pattern 0x7f..f is read as 0x80..0 so that +0 and
+# -0 tie.
+# ---------------------------------------------------------------------------
+def _np_ordered(kind, raw_bits, descending):
+    width = raw_bits.dtype.itemsize * 8
+    ut = raw_bits.dtype.type
+    sign = ut(1 << (width - 1))
+    if kind[0] == "u":
+        o = raw_bits.copy()
+    elif kind[0] == "i":
+        o = raw_bits ^ sign
+    else:
+        neg = (raw_bits & sign) != 0
+        o = np.where(neg, ~raw_bits, raw_bits ^ sign).astype(raw_bits.dtype)
+    if descending:
+        o = ~o
+    if kind[0] == "f":
+        o = np.where(o == ut((1 << (width - 1)) - 1), sign, o).astype(raw_bits.dtype)
+    return o
+
+
+def _np_radix(kind, keys, values, descending, begin, end):
+    bits = _bits(keys)
+    width = bits.dtype.itemsize * 8
+    end = width if end is None else end
+    src = _np_ordered(kind, bits, descending).astype(np.uint64)
+    mask = np.uint64((1 << (end - begin)) - 1) if end - begin < 64 else np.uint64(~0 & (2**64 - 1))
+    digit = (src >> np.uint64(begin)) & mask
+    order = np.argsort(digit, kind="stable")
+    return keys[order], (None if values is None else values[order])
+
+
+def _special_float_keys(kind, n, seed):
+    rng = np.random.default_rng(seed)
+    dt = np.dtype(NP[kind])
+    ut = BITS_OF[dt.itemsize]
+    raw = rng.integers(0, np.iinfo(ut).max, size=n, dtype=ut, endpoint=True)
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, -np.nan, 1.0, -1.0,
+                         np.finfo(dt).tiny, -np.finfo(dt).tiny, np.finfo(dt).max,
+                         np.finfo(dt).smallest_subnormal], dtype=dt).view(ut)
+    pos = rng.integers(0, n, size=n // 3)
+    raw[pos] = specials[rng.integers(0, specials.size, size=pos.size)]
+    return raw.view(dt)
+
+
+@pytest.mark.parametrize("kind", ["u32", "i32", "f32", "u64", "i64", "f64"])
+@pytest.mark.parametrize("descending", [False, True])
+def test_radix_oracle_vs_numpy(kind, descending):
+    n = 20_000
+    dt = np.dtype(NP[kind])
+    width = dt.itemsize * 8
+    rng = np.random.default_rng(7 + width)
+    if dt.kind == "f":
+        keys = _special_float_keys(kind, n, 11 + width)
+    else:
+        ut = BITS_OF[dt.itemsize]
+        keys = rng.integers(0, np.iinfo(ut).max, size=n, dtype=ut, endpoint=True).view(dt)
+        keys[rng.integers(0, n, size=n // 4)] = keys[5]  # heavy ties
+        keys[:4] = np.array([np.iinfo(dt).min, np.iinfo(dt).max, 0, 1], dtype=dt)
+    values = np.arange(n, dtype=np.uint32)
+    for begin, end in [(0, None), (0, width // 2), (3, width - 5), (width - 8, width), (5, 5)]:
+        got_k, got_v = oracle.radix_sort(kind, keys, values, descending, begin, end)
+        want_k, want_v = _np_radix(kind, keys, values, descending, begin, end)
+        assert np.array_equal(_bits(got_k), _bits(want_k)), (begin, end)
+        assert np.array_equal(got_v, want_v), (begin, end)
+
+
+def test_radix_oracle_pairs_probe_family():
+    # rccl-cub/examples/device_radix_sort_pairs_probe.rs:34-176: narrow key
+    # domain, Rust's stable sort_by_key as the reference.
+    idx = np.arange(10_003, dtype=np.uint64)
+    h = (idx * np.uint64(2_654_435_761)) & np.uint64(0xFFFFFFFF)
+    r = idx & np.uint64(31)
+    rot = ((h << r) | (h >> ((np.uint64(32) - r) % np.uint64(32)))) & np.uint64(0xFFFFFFFF)
+    keys = (rot & np.uint64(0x3FF)).astype(np.uint32)
+    values = np.arange(keys.size, dtype=np.int32)
+    pairs = list(zip(keys.tolist(), values.tolist()))
+    asc = sorted(pairs, key=lambda p: p[0])
+    desc = sorted(pairs, key=lambda p: -p[0])
+    k, v = oracle.radix_sort("u32", keys, values)
+    assert list(zip(k.tolist(), v.tolist())) == asc
+    k, v = oracle.radix_sort("u32", keys, values, descending=True)
+    assert list(zip(k.tolist(), v.tolist())) == desc
+    k, v = oracle.radix_sort("u64", keys.astype(np.uint64), values.astype(np.uint64))
+    assert list(zip(k.tolist(), v.tolist())) == asc
+    # :255-305: bit window 0..24 sorts by the low 24 bits only.
+    wk = (((np.arange(10_003, dtype=np.uint64) & np.uint64(0xFF)) << np.uint64(24)) |
+          ((np.arange(10_003, dtype=np.uint64) * np.uint64(97)) & np.uint64(0x3FF))).astype(np.uint32)
+    wv = np.arange(wk.size, dtype=np.int32)
+    for d in (False, True):
+        k, v = oracle.radix_sort("u32", wk, wv, d, 0, 24)
+        exp = sorted(zip(wk.tolist(), wv.tolist()),
+                     key=(lambda p: -(p[0] & 0xFFFFFF)) if d else (lambda p: p[0] & 0xFFFFFF))
+        assert list(zip(k.tolist(), v.tolist())) == exp
+
+
+# ---------------------------------------------------------------------------
+# Merge and merge sort vs the standard library.
+# ---------------------------------------------------------------------------
+def _int_keys(kind, n, rng, domain):
+    dt = np.dtype(NP[kind])
+    lo = 0 if dt.kind == "u" else -domain // 2
+    return rng.integers(lo, lo + domain, size=n).astype(dt)
+
+
+@pytest.mark.parametrize("kind", ["u8", "i16", "u32", "i64", "f32", "f64"])
+@pytest.mark.parametrize("descending", [False, True])
+def test_merge_oracle_vs_heapq(kind, descending):
+    rng = np.random.default_rng(3)
+    for na, nb, domain in [(0, 0, 5), (0, 9, 5), (13, 0, 5), (500, 700, 20), (3000, 2000, 100)]:
+        a = np.sort(_int_keys(kind, na, rng, domain), kind="stable")
+        b = np.sort(_int_keys(kind, nb, rng, domain), kind="stable")
+        if descending:
+            a, b = a[::-1].copy(), b[::-1].copy()
+        av = np.arange(na, dtype=np.uint32)
+        bv = (np.arange(nb) | (1 << 31)).astype(np.uint32)
+        want = list(heapq.merge(zip(a.tolist(), av.tolist()), zip(b.tolist(), bv.tolist()),
+                                key=lambda p: p[0], reverse=descending))
+        k, v = oracle.merge(kind, a, b, av, bv, descending)
+        assert list(zip(k.tolist(), v.tolist())) == want
+
+
+@pytest.mark.parametrize("kind", ["i8", "u16", "i32", "u64", "f32", "f64"])
+@pytest.mark.parametrize("descending", [False, True])
+def test_merge_sort_oracle_vs_sorted(kind, descending):
+    rng = np.random.default_rng(5)
+    for n, domain in [(0, 3), (1, 3), (2, 3), (1000, 10), (7000, 5000)]:
+        keys = _int_keys(kind, n, rng, domain)
+        vals = np.arange(n, dtype=np.uint64)
+        want = sorted(zip(keys.tolist(), vals.tolist()), key=lambda p: p[0], reverse=descending)
+        k, v = oracle.merge_sort(kind, keys, vals, descending)
+        assert list(zip(k.tolist(), v.tolist())) == want
+        assert np.array_equal(oracle.merge_sort(kind, keys, descending=descending), k)
+
+
+# ---------------------------------------------------------------------------
+# Set operations vs multiset algebra and a per-run value rule.
+# ---------------------------------------------------------------------------
+def _runs(keys, vals):
+    """Group a sorted sequence into {key: [values in order]}."""
+    out = collections.OrderedDict()
+    for k, v in zip(keys, vals):
+        out.setdefault(k, []).append(v)
+    return out
+
+
+def _set_by_runs(op, a, av, b, bv, descending):
+    """For a key with m items in A and n in B: union keeps all m of A's then
+    B's last n-m; intersection A's first min(m, n); difference A's last
+    m-n; symmetric difference the longer side's last |m-n|. Keys come out in
+    the sequence order (rccl-cub/src/ordering_backend/set.rs:564-827)."""
+    ra, rb = _runs(a, av), _runs(b, bv)
+    keys = sorted(set(ra) | set(rb), reverse=descending)
+    ok, ov = [], []
+    for k in keys:
+        xa, xb = ra.get(k, []), rb.get(k, [])
+        m, n = len(xa), len(xb)
+        if op == "union":
+            take = xa + xb[m:] if n > m else xa
+        elif op == "intersection":
+            take = xa[:min(m, n)]
+        elif op == "difference":
+            take = xa[n:] if m > n else []
+        else:
+            take = xa[n:] if m > n else xb[m:]
+        ok += [k] * len(take)
+        ov += take
+    return ok, ov
+
+
+@pytest.mark.parametrize("kind", ["u8", "i16", "i32", "u64", "f64"])
+@pytest.mark.parametrize("op", OPS)
+def test_set_oracle_vs_multiset_algebra(kind, op):
+    rng = np.random.default_rng(11)
+    for na, nb, domain in [(0, 0, 4), (0, 50, 4), (60, 0, 4), (700, 900, 12), (4000, 3000, 300)]:
+        for descending in (False, True):
+            a = np.sort(_int_keys(kind, na, rng, domain), kind="stable")
+            b = np.sort(_int_keys(kind, nb, rng, domain), kind="stable")
+            if descending:
+                a, b = a[::-1].copy(), b[::-1].copy()
+            av = np.arange(na, dtype=np.int32)
+            bv = (np.arange(nb) + 1_000_000).astype(np.int32)
+            k, v = oracle.set_op(op, kind, a, b, av, bv, descending)
+            ca, cb = collections.Counter(a.tolist()), collections.Counter(b.tolist())
+            counts = {"union": ca | cb, "intersection": ca & cb, "difference": ca - cb,
+                      "symmetric_difference": (ca - cb) + (cb - ca)}[op]
+            assert collections.Counter(k.tolist()) == counts
+            wk, wv = _set_by_runs(op, a.tolist(), av.tolist(), b.tolist(), bv.tolist(), descending)
+            assert k.tolist() == wk and v.tolist() == wv
+            assert oracle.set_op(op, kind, a, b, descending=descending, count_only=True) == len(wk)
+
+
+def test_set_oracle_reference_families():
+    # rccl-thrust/examples/set_operations_tests.rs:491-590
+    n = 25_000
+    evens = (np.arange(n) * 2).astype(np.int32)
+    odds = evens + 1
+    assert np.array_equal(oracle.set_op("union", "i32", evens, odds),
+                          np.arange(2 * n, dtype=np.int32))
+    assert oracle.set_op("intersection", "i32", evens, odds).size == 0
+    assert np.array_equal(oracle.set_op("union", "i32", evens, evens), evens)
+    assert oracle.set_op("difference", "i32", evens, evens).size == 0
+    first = sorted(((i * 37 + 11) % 13) - 6 for i in range(4097))
+    second_all = sorted(((i * 29 + 7) % 13) - 6 for i in range(8194))
+    for second_len in [0, 1, 2048, 4097, 4098, 8194]:
+        second = second_all[:second_len]
+        ca, cb = collections.Counter(first), collections.Counter(second)
+        for op, c in [("union", ca | cb), ("intersection", ca & cb), ("difference", ca - cb),
+                      ("symmetric_difference", (ca - cb) + (cb - ca))]:
+            got = oracle.set_op(op, "i32", np.array(first, np.int32), np.array(second, np.int32))
+            assert got.tolist() == sorted(c.elements())
+
+
+def test_splitmix64_known_answer():
+    # splitmix64 finaliser of state 0 (Steele, Lea and Flood 2014; the
+    # constants of Java's SplittableRandom).
+    assert oracle.splitmix64(0) == 0xE220A8397B1DCDAF
