@@ -3,14 +3,17 @@
 
 Metric: Gkeys/s radix sort at 2^28 for u32 keys (the headline
 ``value``) and for u64-key/u32-value pairs (reported under ``pairs``), with the
-fraction of the 8 TB/s HBM roofline.
+fraction of the 8 TB/s HBM roofline. The C4 merge / merge sort and C5 set
+operation shapes are reported under ``ordering``.
 
-A step is one full radix sort of the resident 2^28-item input. The sort is in
-place, so before every step the input is restored from a pristine device copy;
-that copy is outside the HIP-event interval that times the sort
+A step is one full pass of the operation over the resident input. Radix sort
+is in place, so before every step its input is restored from a pristine
+device copy; that copy is outside the HIP-event interval that times the sort
 (``ms_per_step``) and inside the wall-clock interval (``ms_per_step_wall``).
 Per-launch kernel durations come from the library's own hipEvent timing
-(rccl_hip_timing_enable), recorded on the sort's stream during the timed steps.
+(rccl_hip_timing_enable), recorded on the launch stream during the timed
+steps. Inputs are generated on the device (rccl_amd.workloads_device, bit-
+identical to the host generators the tests use).
 """
 from __future__ import annotations
 
@@ -28,52 +31,41 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "Gkeys/s radix sort (u32 keys; u64+u32 pairs) at 2^28; % of HBM roofline"
 
 
-def _hash_check(torch, t):
-    """Order-independent fingerprint of a device tensor: wrapping sums of the
-    words and of their squares."""
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _fingerprint(torch, t):
+    """Order-independent fingerprint: wrapping sums of the words and squares."""
     w = t.to(torch.int64)
-    return int(w.sum().item()), int((w * w).sum().item())
+    m = (1 << 64) - 1
+    return int(w.sum().item()) & m, int((w * w).sum().item()) & m
 
 
-def _sorted_unsigned(torch, t, bits):
+def _nondecreasing(torch, t, bits):
     """True if the unsigned view of t is non-decreasing."""
+    if t.numel() < 2:
+        return True
     if bits == 32:
         u = t.to(torch.int64) & 0xFFFFFFFF
         return bool((u[1:] >= u[:-1]).all().item())
-    # u64: compare with the sign bit flipped so signed order equals unsigned order.
     s = t ^ torch.tensor(-(1 << 63), dtype=torch.int64, device=t.device)
     return bool((s[1:] >= s[:-1]).all().item())
 
 
-def run_sort(torch, cub, abi, DeviceBuffer, keys_h, values_h, steps, warmup, label):
-    n = keys_h.size
-    launch = cub.Program.load(0).on(torch.cuda.current_stream(0))
-    stream = launch.stream()
-    pristine_k = DeviceBuffer.from_host(keys_h)
-    keys = DeviceBuffer.empty(keys_h.dtype, n)
-    if values_h is not None:
-        pristine_v = DeviceBuffer.from_host(values_h)
-        values = DeviceBuffer.empty(values_h.dtype, n)
-        ws = cub.device_radix_sort_pairs_workspace(launch, keys_h.dtype, values_h.dtype, n)
-    else:
-        ws = cub.device_radix_sort_workspace(launch, keys_h.dtype, n)
+def _buffer(torch, DeviceBuffer, t, np_dtype):
+    """Wrap a device tensor (same-width signed storage) as a DeviceBuffer."""
+    return DeviceBuffer(t.contiguous(), np_dtype, t.numel())
 
-    def restore():
-        keys.copy_from(pristine_k)
-        if values_h is not None:
-            values.copy_from(pristine_v)
 
-    def sort():
-        if values_h is not None:
-            cub.device_radix_sort_pairs(launch, keys, values, ws)
-        else:
-            cub.device_radix_sort_keys(launch, keys, ws)
-
+def time_steps(torch, abi, stream, steps, warmup, step, before=None):
+    """Run `step` warmup + steps times; returns (mean event ms, min, wall ms,
+    {kernel: mean ms}, {kernel: launches per step})."""
     for _ in range(warmup):
-        restore()
-        sort()
+        if before:
+            before()
+        step()
     torch.cuda.synchronize()
-
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     abi.timing_read()
@@ -81,75 +73,29 @@ def run_sort(torch, cub, abi, DeviceBuffer, keys_h, values_h, steps, warmup, lab
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(steps):
-        restore()
+        if before:
+            before()
         starts[k].record(stream)
-        sort()
+        step()
         ends[k].record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     abi.timing_enable(False)
     records = abi.timing_read()
     step_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    ms = sum(step_ms) / len(step_ms)
-
-    kernel_ms = {}
+    per = {}
     for name, kms, _items in records:
-        kernel_ms.setdefault(name, []).append(kms)
-
-    # Validate the last step's output: sorted, and the same multiset of keys
-    # (fingerprints) and of values.
-    bits = keys_h.dtype.itemsize * 8
-    ok = _sorted_unsigned(torch, keys.tensor[:n] if bits == 64 else keys.tensor, bits)
-    ok = ok and _hash_check(torch, keys.tensor) == _hash_check(torch, pristine_k.tensor)
-    if values_h is not None:
-        ok = ok and _hash_check(torch, values.tensor) == _hash_check(torch, pristine_v.tensor)
-    del pristine_k, keys
-    if values_h is not None:
-        del pristine_v, values
-    torch.cuda.empty_cache()
-    return {
-        "label": label,
-        "n": n,
-        "ms": ms,
-        "ms_min": min(step_ms),
-        "ms_wall": (t1 - t0) * 1e3 / steps,
-        "kernel_ms": {k: sum(v) / len(v) for k, v in kernel_ms.items()},
-        "kernel_launches": {k: len(v) for k, v in kernel_ms.items()},
-        "validated": bool(ok),
-    }
+        per.setdefault(name, []).append(kms)
+    return (sum(step_ms) / steps, min(step_ms), (t1 - t0) * 1e3 / steps,
+            {k: sum(v) / len(v) for k, v in per.items()},
+            {k: len(v) // steps for k, v in per.items()})
 
 
-def cpu_baseline(keys_h, values_h, seconds, log2_sample):
-    """Oracle LSD radix sort (single thread) on the first 2^log2_sample items
-    of the same input, repeated for about `seconds`."""
-    import oracle
-
-    n = min(keys_h.size, 1 << log2_sample)
-    k = keys_h[:n].copy()
-    v = None if values_h is None else values_h[:n].copy()
-    kind = "u32" if k.dtype.itemsize == 4 else "u64"
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        oracle.radix_sort(kind, k, v)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    gk = reps * n / el / 1e9
-    return {
-        "value": round(gk, 4),
-        "unit": "Gkeys/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"oracle/oracle.c stable LSD radix sort (8-bit passes), first 2^{log2_sample} "
-                  f"{'keys' if v is None else 'pairs'} of the benchmark input, {reps} sorts in "
-                  f"{el:.1f} s",
-    }
-
-
-def roofline(bytes_per_launch, launch_ms, traffic=None):
+def roofline(bytes_per_launch, launch_ms, kernel, traffic=None):
     achieved = bytes_per_launch / (launch_ms * 1e-3) / 1e9
+    extra = {} if traffic is None else {
+        "traffic_source": "profiles/hbm_traffic_2p28.txt (rocprofv3 FETCH_SIZE x 2.0 + "
+                          "WRITE_SIZE x 1.0, calibrated on a 1 GiB copy)"}
     return {
         "bound": "hbm",
         "achieved": round(achieved, 1),
@@ -157,6 +103,204 @@ def roofline(bytes_per_launch, launch_ms, traffic=None):
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": traffic,
+        "kernel": kernel,
+        **extra,
+    }
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_2p28.txt")
+
+
+def profiled_traffic(kernel, log2n):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE scaled by a copy kernel of known size),
+    or None when that summary does not cover this problem size."""
+    if log2n != 28 or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    with open(TRAFFIC_PROFILE) as f:
+        for line in f:
+            parts = line.split()
+            if parts and parts[0] == kernel and len(parts) >= 7:
+                return int(parts[6])
+    return None
+
+
+def _rounded(d):
+    return {k: round(v, 4) for k, v in d.items()}
+
+
+# ---------------------------------------------------------------------------
+# Radix sort legs (the metric).
+# ---------------------------------------------------------------------------
+def run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, values_t, steps, warmup):
+    n = keys_t.numel()
+    launch = cub.Program.load(0).on(torch.cuda.current_stream(0))
+    kdt = np.uint32 if keys_t.dtype == torch.int32 else np.uint64
+    pristine_k = keys_t
+    keys = _buffer(torch, DeviceBuffer, torch.empty_like(keys_t), kdt)
+    if values_t is not None:
+        pristine_v = values_t
+        values = _buffer(torch, DeviceBuffer, torch.empty_like(values_t), np.uint32)
+        ws = cub.device_radix_sort_pairs_workspace(launch, kdt, np.uint32, n)
+    else:
+        ws = cub.device_radix_sort_workspace(launch, kdt, n)
+
+    def restore():
+        keys.tensor.copy_(pristine_k)
+        if values_t is not None:
+            values.tensor.copy_(pristine_v)
+
+    def sort():
+        if values_t is not None:
+            cub.device_radix_sort_pairs(launch, keys, values, ws)
+        else:
+            cub.device_radix_sort_keys(launch, keys, ws)
+
+    ms, ms_min, wall, kms, launches = time_steps(torch, abi, launch.stream(), steps, warmup,
+                                                 sort, restore)
+    bits = 32 if kdt == np.uint32 else 64
+    ok = _nondecreasing(torch, keys.tensor, bits)
+    ok = ok and _fingerprint(torch, keys.tensor) == _fingerprint(torch, pristine_k)
+    if values_t is not None:
+        ok = ok and _fingerprint(torch, values.tensor) == _fingerprint(torch, pristine_v)
+    return {"n": n, "ms": ms, "ms_min": ms_min, "ms_wall": wall, "kernel_ms": kms,
+            "launches": launches, "validated": bool(ok)}
+
+
+def cpu_baseline(keys_h, seconds, log2_sample):
+    """Oracle LSD radix sort (single thread) on the first 2^log2_sample keys
+    of the same input, repeated for about `seconds`."""
+    import oracle
+
+    n = keys_h.size
+    k = keys_h.copy()
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.radix_sort("u32", k)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {
+        "value": round(reps * n / el / 1e9, 4),
+        "unit": "Gkeys/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"oracle/oracle.c stable LSD radix sort (8-bit passes) over the first "
+                  f"2^{log2_sample} keys of the benchmark input, {reps} sorts in {el:.1f} s",
+    }
+
+
+# ---------------------------------------------------------------------------
+# C4 merge and merge sort, C5 set operations.
+# ---------------------------------------------------------------------------
+def run_merge(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup):
+    n_each = 1 << log2_each
+    a, pa, b, pb = wd.c4_merge_inputs(n_each)
+    launch = cub.Program.load(0).on(torch.cuda.current_stream(0))
+    A, PA, B, PB = (_buffer(torch, DeviceBuffer, t, np.uint32) for t in (a, pa, b, pb))
+    out = DeviceBuffer.empty(np.uint32, 2 * n_each)
+    outv = DeviceBuffer.empty(np.uint32, 2 * n_each)
+    ws = cub.device_merge_pairs_workspace(launch, np.uint32, np.uint32, n_each, n_each)
+
+    def step():
+        cub.device_merge_pairs(launch, A, PA, B, PB, ws, out, outv)
+
+    ms, ms_min, wall, kms, launches = time_steps(torch, abi, launch.stream(), steps, warmup, step)
+    total = 2 * n_each
+    ok = _nondecreasing(torch, out.tensor, 32)
+    ok = ok and _fingerprint(torch, out.tensor) == tuple(
+        (x + y) & ((1 << 64) - 1) for x, y in zip(_fingerprint(torch, a), _fingerprint(torch, b)))
+    # Stability: on equal keys every A payload (high bit clear) precedes B's.
+    k64 = out.tensor.to(torch.int64) & 0xFFFFFFFF
+    src_b = (outv.tensor < 0)
+    same = k64[1:] == k64[:-1]
+    ok = ok and not bool((same & src_b[:-1] & ~src_b[1:]).any().item())
+    res = {
+        "workload": f"C4 DeviceMerge pairs: two sorted u32 arrays of 2^{log2_each} in [0, 2^24), "
+                    "u32 payloads marking the source",
+        "value": round(total / (ms * 1e-3) / 1e9, 3), "unit": "Gkeys/s (outputs)",
+        "ms_per_step": round(ms, 4), "ms_per_step_wall": round(wall, 4),
+        "bytes_model": "16 B/output = 8 B read (key + value) + 8 B written",
+        "roofline": roofline(16.0 * total, kms["merge"], "merge (one launch merges everything)"),
+        "kernel_ms": _rounded(kms), "validated": bool(ok),
+    }
+    del a, pa, b, pb, A, PA, B, PB, out, outv, ws
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_merge_sort(torch, np, cub, abi, DeviceBuffer, wd, log2n, steps, warmup):
+    n = 1 << log2n
+    keys_t = wd.c4_merge_sort_keys(n)
+    launch = cub.Program.load(0).on(torch.cuda.current_stream(0))
+    src = _buffer(torch, DeviceBuffer, keys_t, np.uint32)
+    out = DeviceBuffer.empty(np.uint32, n)
+    ws = cub.device_merge_sort_workspace(launch, np.uint32, n)
+
+    def step():
+        cub.device_merge_sort_keys_copy(launch, src, ws, out)
+
+    ms, ms_min, wall, kms, launches = time_steps(torch, abi, launch.stream(), steps, warmup, step)
+    ok = _nondecreasing(torch, out.tensor, 32)
+    ok = ok and _fingerprint(torch, out.tensor) == _fingerprint(torch, keys_t)
+    passes = launches.get("merge_sort_pass", 0)
+    res = {
+        "workload": f"C4 DeviceMergeSort keys: 2^{log2n} u32 keys in [0, 2^24), ascending "
+                    "(copy form: input left untouched)",
+        "value": round(n / (ms * 1e-3) / 1e9, 3), "unit": "Gkeys/s",
+        "ms_per_step": round(ms, 4), "ms_per_step_wall": round(wall, 4),
+        "merge_passes": passes,
+        "bytes_model": f"{8 * (1 + passes)} B/key = 8 B (block sort) + 8 B per merge pass",
+        "roofline": roofline(8.0 * n, kms["merge_sort_pass"],
+                             "merge_sort_pass (one pass: 4n read + 4n write)"),
+        "sort_roofline_frac": round(8.0 * (1 + passes) * n / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "kernel_ms": _rounded(kms), "validated": bool(ok),
+    }
+    del keys_t, src, out, ws
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_set_ops(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup):
+    n_each = 1 << log2_each
+    a, b = wd.c5_inputs(n_each)
+    launch = cub.Program.load(0).on(torch.cuda.current_stream(0))
+    A, B = (_buffer(torch, DeviceBuffer, t, np.uint64) for t in (a, b))
+    out = DeviceBuffer.empty(np.uint64, 2 * n_each)
+    # Reference counts from a device histogram of both multisets.
+    u, inv = torch.unique(torch.cat([a, b]), return_inverse=True)
+    ca = torch.bincount(inv[:n_each], minlength=u.numel())
+    cb = torch.bincount(inv[n_each:], minlength=u.numel())
+    want = {"union": int(torch.maximum(ca, cb).sum()), "intersection": int(torch.minimum(ca, cb).sum()),
+            "difference": int((ca - cb).clamp(min=0).sum()),
+            "symmetric_difference": int((ca - cb).abs().sum())}
+    del u, inv, ca, cb
+    results = {}
+    for op in ("union", "intersection", "difference", "symmetric_difference"):
+        ws = cub.device_set_workspace(launch, op, np.uint64, n_each, n_each)
+
+        def step(op=op, ws=ws):
+            cub.device_set_keys(launch, op, A, B, ws, out)
+
+        ms, ms_min, wall, kms, _ = time_steps(torch, abi, launch.stream(), steps, warmup, step)
+        m = ws.count()
+        ok = m == want[op] and _nondecreasing(torch, out.tensor[:m], 64)
+        results[op] = {
+            "ms_per_step": round(ms, 4), "output": m,
+            "value": round(2 * n_each / (ms * 1e-3) / 1e9, 3), "unit": "Gkeys/s (inputs)",
+            "roofline": roofline(16.0 * n_each + 8.0 * m, kms["set_tile"],
+                                 "set_tile (reads both inputs, writes the result)"),
+            "kernel_ms": _rounded(kms), "validated": bool(ok),
+        }
+    del a, b, A, B, out
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"C5 set operations, keys only: sorted u64 multisets of 2^{log2_each} each "
+                    "(shared pool, ~10% duplicated runs)",
+        "bytes_model": "8 B read per input key + 8 B written per output key",
+        **results,
     }
 
 
@@ -167,6 +311,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--log2n", type=int, default=28)
     ap.add_argument("--no-pairs", action="store_true", help="skip the u64+u32 pairs leg")
+    ap.add_argument("--no-ordering", action="store_true",
+                    help="skip the C4 merge / merge sort and C5 set operation legs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -175,26 +321,31 @@ def main():
               "(this build has no multi-GPU path).", file=sys.stderr)
         return 2
 
+    import numpy as np
     import torch
 
     from rccl_amd import _abi as abi
     from rccl_amd import cub, workloads
+    from rccl_amd import workloads_device as wd
     from rccl_amd.device import DeviceBuffer
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     n = 1 << args.log2n
-    print(f"[bench] generating inputs n=2^{args.log2n}", file=sys.stderr, flush=True)
-    keys_h = workloads.metric_u32_keys(n)
-    r32 = run_sort(torch, cub, abi, DeviceBuffer, keys_h, None, args.steps, args.warmup, "u32")
-    print(f"[bench] u32 keys: {r32['ms']:.3f} ms/sort", file=sys.stderr, flush=True)
+    _log(f"u32 keys n=2^{args.log2n}")
+    keys_t = wd.metric_u32_keys(n)
+    r32 = run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, None, args.steps, args.warmup)
+    del keys_t
+    _log(f"u32 keys: {r32['ms']:.3f} ms/sort")
 
     rp = None
     if not args.no_pairs:
-        pk, pv = workloads.metric_pairs(n)
-        rp = run_sort(torch, cub, abi, DeviceBuffer, pk, pv, args.steps, args.warmup, "pairs")
-        print(f"[bench] u64+u32 pairs: {rp['ms']:.3f} ms/sort", file=sys.stderr, flush=True)
+        pk, pv = wd.metric_pairs(n)
+        rp = run_radix(torch, np, cub, abi, DeviceBuffer, pk, pv, args.steps, args.warmup)
+        del pk, pv
+        _log(f"u64+u32 pairs: {rp['ms']:.3f} ms/sort")
+    torch.cuda.empty_cache()
 
     gkeys = n / (r32["ms"] * 1e-3) / 1e9
     out = {
@@ -218,15 +369,16 @@ def main():
             "bytes_model": "36 B/key = 4n (histogram read) + 4 x (4n read + 4n write)",
         },
         "sort_roofline_frac": round(36.0 * n / (r32["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": roofline(8.0 * n, r32["kernel_ms"]["radix_onesweep"]),
-        "kernel_ms": {k: round(v, 4) for k, v in r32["kernel_ms"].items()},
+        "roofline": roofline(8.0 * n, r32["kernel_ms"]["radix_onesweep"],
+                             "radix_onesweep (one 8-bit pass: 4n read + 4n write)",
+                             profiled_traffic("radix_onesweep_u32", args.log2n)),
+        "kernel_ms": _rounded(r32["kernel_ms"]),
         "validated": r32["validated"],
     }
-    out["roofline"]["kernel"] = "radix_onesweep (one 8-bit pass: 4n read + 4n write)"
+    valid = r32["validated"]
     if rp is not None:
-        pg = n / (rp["ms"] * 1e-3) / 1e9
         out["pairs"] = {
-            "value": round(pg, 3),
+            "value": round(n / (rp["ms"] * 1e-3) / 1e9, 3),
             "unit": "Gkeys/s",
             "ms_per_step": round(rp["ms"], 4),
             "ms_per_step_wall": round(rp["ms_wall"], 4),
@@ -235,16 +387,38 @@ def main():
                                    f"u32 values = index, n=2^{args.log2n}, 8 passes",
                        "bytes_model": "200 B/pair = 8n + 8 x (12n read + 12n write)"},
             "sort_roofline_frac": round(200.0 * n / (rp["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "roofline": roofline(24.0 * n, rp["kernel_ms"]["radix_onesweep"]),
-            "kernel_ms": {k: round(v, 4) for k, v in rp["kernel_ms"].items()},
+            "roofline": roofline(24.0 * n, rp["kernel_ms"]["radix_onesweep"],
+                                 "radix_onesweep (one pass: 12n read + 12n write)",
+                                 profiled_traffic("radix_onesweep_pairs", args.log2n)),
+            "kernel_ms": _rounded(rp["kernel_ms"]),
             "validated": rp["validated"],
         }
-        out["pairs"]["roofline"]["kernel"] = "radix_onesweep (one pass: 12n read + 12n write)"
+        valid = valid and rp["validated"]
+    if not args.no_ordering:
+        log_each = max(args.log2n - 1, 1)
+        log_sort = max(args.log2n - 2, 1)
+        _log("C4 merge")
+        mg = run_merge(torch, np, cub, abi, DeviceBuffer, wd, log_each, args.steps, args.warmup)
+        _log(f"C4 merge: {mg['ms_per_step']:.3f} ms")
+        _log("C4 merge sort")
+        ms = run_merge_sort(torch, np, cub, abi, DeviceBuffer, wd, log_sort, args.steps,
+                            args.warmup)
+        _log(f"C4 merge sort: {ms['ms_per_step']:.3f} ms")
+        _log("C5 set operations")
+        so = run_set_ops(torch, np, cub, abi, DeviceBuffer, wd, log_sort, args.steps, args.warmup)
+        _log("C5 set operations done")
+        out["ordering"] = {"merge": mg, "merge_sort": ms, "set_ops": so}
+        valid = valid and mg["validated"] and ms["validated"] and all(
+            so[op]["validated"] for op in ("union", "intersection", "difference",
+                                           "symmetric_difference"))
     if not args.no_cpu_baseline:
-        print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(keys_h, None, args.cpu_seconds, 24)
+        _log("cpu baseline")
+        log_sample = min(24, args.log2n)
+        out["cpu_baseline"] = cpu_baseline(workloads.metric_u32_keys(1 << log_sample),
+                                           args.cpu_seconds, log_sample)
+    out["validated"] = bool(valid)
     print(json.dumps(out), flush=True)
-    return 0 if out["validated"] and (rp is None or rp["validated"]) else 1
+    return 0 if valid else 1
 
 
 if __name__ == "__main__":

@@ -4,6 +4,15 @@
  * TEST INFRASTRUCTURE ONLY: the checker for tests/, __graft_entry__.smoke()
  * and bench.py's cpu_baseline leg. The product never links or calls it.
  * Reference paths below are relative to the StarGazerM/rccl tree.
+ *
+ * Pinning (tests/test_oracle.py): every function is checked against the
+ * reference's literal probe/test vectors (tests/golden/reference_vectors.json)
+ * and against an independent restatement (numpy key transform + stable
+ * argsort, heapq.merge, sorted, multiset algebra with a per-run value rule).
+ * Parity unpinned: NaN keys in oracle_merge, oracle_merge_sort and
+ * oracle_set_op (IEEE '<' makes NaN equivalent to every key, so the result
+ * depends on the merge and balanced paths; no reference vector covers it).
+ * Radix order of NaN bit patterns is pinned.
  */
 #include "oracle.h"
 

@@ -159,3 +159,27 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=600)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+def _same_bits(t, host):
+    import torch  # noqa: F401
+    a = t.cpu().numpy()
+    return np.array_equal(a.view(np.dtype(f"u{a.dtype.itemsize}")),
+                          host.view(np.dtype(f"u{host.dtype.itemsize}")))
+
+
+def test_device_generators_match_host_on_cpu():
+    """The benchmark's device-side generators (run here by torch on the CPU)
+    produce exactly the host generators' bits."""
+    from rccl_amd import workloads_device as wd
+    n = 1 << 14
+    assert _same_bits(wd.hash_range(99, n, 5, "cpu"), workloads.hash_range(99, n, 5))
+    assert _same_bits(wd.metric_u32_keys(n, "cpu"), workloads.metric_u32_keys(n))
+    k, v = wd.metric_pairs(n, "cpu")
+    hk, hv = workloads.metric_pairs(n)
+    assert _same_bits(k, hk) and _same_bits(v, hv)
+    for d, h in zip(wd.c4_merge_inputs(n, "cpu"), workloads.c4_merge_inputs(n)):
+        assert _same_bits(d, h)
+    assert _same_bits(wd.c4_merge_sort_keys(n, "cpu"), workloads.c4_merge_sort_keys(n))
+    for d, h in zip(wd.c5_inputs(n, "cpu"), workloads.c5_inputs(n)):
+        assert _same_bits(d, h)

@@ -221,3 +221,46 @@ def test_window_noop_and_invalid(launch):
     cub.device_radix_sort_keys_buffer(launch, buffers, range(0, 8), ws)
     launch.synchronize()
     np.testing.assert_array_equal(buffers.current().to_host_vec(), [1, 3, 7, 9])
+
+
+@pytest.mark.parametrize("dtype,vdtype,n,window,flipped", [
+    (np.uint32, None, 100, (0, 32), True),
+    (np.uint32, None, 4864, (0, 32), True),
+    (np.uint32, None, 4865, (0, 32), False),
+    (np.uint32, None, 100, (0, 24), True),
+    (np.uint64, None, 2304, (0, 64), True),
+    (np.uint64, None, 2305, (0, 64), False),
+    (np.uint32, np.uint64, 2304, (0, 32), True),
+    (np.uint32, np.uint64, 2305, (0, 32), False),
+    (np.int32, np.uint32, 4864, (0, 16), True),
+])
+def test_double_buffer_selector_parity(launch, dtype, vdtype, n, window, flipped):
+    """The selector ends where the reference leaves it: its single-tile route
+    (n <= 256 * 19 * 4 / max(item bytes, 4), rccl-cub/src/workspace.rs:22-66)
+    flips once, the onesweep route once per 8-bit pass
+    (rccl-cub/src/radix.rs:470-548)."""
+    raw = (np.arange(n, dtype=np.uint64) * np.uint64(0x9E3779B97F4A7C15)) >> np.uint64(17)
+    host = raw.astype(np.dtype(dtype).str.replace("i", "u")).view(dtype)
+    kind = _kind(host)
+    k0, k1 = DeviceBuffer.from_host(host), DeviceBuffer.zeroed(dtype, n)
+    if vdtype is None:
+        buffers = cub.DoubleBuffer.new(k0, k1)
+        ws = cub.device_radix_sort_keys_buffer_workspace(launch, dtype, n)
+        cub.device_radix_sort_keys_buffer(launch, buffers, range(*window), ws)
+        launch.synchronize()
+        got = buffers.current().to_host_vec()
+        want = oracle.radix_sort(kind, host, begin_bit=window[0], end_bit=window[1])
+    else:
+        vals = np.arange(n, dtype=vdtype)
+        v0, v1 = DeviceBuffer.from_host(vals), DeviceBuffer.zeroed(vdtype, n)
+        buffers = cub.DoubleBuffer.paired((k0, v0), (k1, v1))
+        ws = cub.device_radix_sort_pairs_buffer_workspace(launch, dtype, vdtype, n)
+        cub.device_radix_sort_pairs_buffer(launch, buffers, range(*window), ws)
+        launch.synchronize()
+        ck, cv = buffers.current()
+        got = ck.to_host_vec()
+        want, want_v = oracle.radix_sort(kind, host, vals, begin_bit=window[0],
+                                         end_bit=window[1])
+        np.testing.assert_array_equal(cv.to_host_vec(), want_v)
+    np.testing.assert_array_equal(_bits(got), _bits(want))
+    assert buffers.current_is_first() == (not flipped)
