@@ -22,6 +22,9 @@ SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # gfx950 only. Packed FP32 instructions are disabled for all device code.
+# The atomic optimizer is off: it rewrites single-lane atomics into a
+# wave-wide sequence that consumes the returned value at once, which turns
+# the onesweep's early tile claim into a full memory-counter wait.
 COMPILE_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
@@ -32,6 +35,7 @@ COMPILE_FLAGS = [
     "-I" + INCLUDE,
     "-I" + CSRC,
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 ]
 
 

@@ -98,7 +98,7 @@ template <class Desc> struct LookbackBuf {
 #define RCCL_RADIX_ITEMS_8B 12
 #endif
 #ifndef RCCL_RADIX_ITEMS_16B
-#define RCCL_RADIX_ITEMS_16B 8
+#define RCCL_RADIX_ITEMS_16B 7
 #endif
 #ifndef RCCL_RADIX_LOOKBACK_WINDOW
 #define RCCL_RADIX_LOOKBACK_WINDOW 16
@@ -108,6 +108,20 @@ template <class Desc> struct LookbackBuf {
 #endif
 #ifndef RCCL_RADIX_LOOKBACK_GROUP
 #define RCCL_RADIX_LOOKBACK_GROUP 16
+#endif
+// Where the next tile is claimed: 0 at the start of a tile, 1 after its
+// ranking, 2 at its staging (the prefetch of the next tile's keys then
+// follows the look-back).
+#ifndef RCCL_RADIX_CLAIM_POINT
+#define RCCL_RADIX_CLAIM_POINT 1
+#endif
+// 1: a persistent grid whose blocks loop over tiles, claiming the next tile
+// one ahead and prefetching its keys; 0: one tile per block.
+#ifndef RCCL_RADIX_PERSISTENT
+#define RCCL_RADIX_PERSISTENT 0
+#endif
+#ifndef RCCL_RADIX_LDS_BATCH
+#define RCCL_RADIX_LDS_BATCH 8
 #endif
 #ifndef RCCL_RADIX_GROUP_WINDOW
 #define RCCL_RADIX_GROUP_WINDOW 4
@@ -192,6 +206,28 @@ histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__
   }
 }
 
+// Turn every pass's digit counts into exclusive offsets (the first output
+// position of each digit), once, so the onesweep blocks read them instead of
+// each scanning the bins. One block of BINS threads. (Internal linkage, like
+// init_kernel.)
+namespace {
+__global__ void __launch_bounds__(BINS) bins_scan_kernel(uint32_t *bins, uint32_t passes) {
+  __shared__ uint32_t s_wave[BINS / 64];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  for (uint32_t p = 0; p < passes; ++p) {
+    const uint32_t c = bins[p * BINS + tid];
+    const uint32_t inc = wave_inclusive_sum(c, lane);
+    if (lane == 63) s_wave[tid >> 6] = inc;
+    __syncthreads();
+    uint32_t excl = inc - c;
+    for (uint32_t w = 0; w < (tid >> 6); ++w) excl += s_wave[w];
+    bins[p * BINS + tid] = excl;
+    __syncthreads();
+  }
+}
+} // namespace
+
 // ---------------------------------------------------------------------------
 // onesweep: one stable counting-sort pass. Persistent blocks claim tiles of
 // THREADS*ITEMS keys in order from an atomic counter and software-pipeline
@@ -208,8 +244,13 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
                 uint32_t bit, uint32_t mask) {
   constexpr bool PAIRS = !std::is_same<Val, NoValue>::value;
   constexpr int WAVES = THREADS / 64;
+  // Ranking works on 32-lane halves of each wave ("sub-waves"), each owning a
+  // contiguous chunk of 32 * ITEMS keys.
+  constexpr int SUBS = 2 * WAVES;
   constexpr int TILE = THREADS * ITEMS;
-  constexpr int WAVE_ITEMS = 64 * ITEMS;
+  constexpr int SUB_ITEMS = 32 * ITEMS;
+  // LDS reads issued back to back before their results are used.
+  constexpr int BATCH = RCCL_RADIX_LDS_BATCH;
   // Items past the end of the input (last tile only) rank in an extra
   // dummy bin and stage into one spare slot, so the loops need no branches.
   constexpr int NB = BINS + 1;
@@ -222,14 +263,17 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   using DI = DescInfo<Desc>;
   using ValReg = typename std::conditional<PAIRS, Val, char>::type;
 
-  // The match masks (ranking) and the staged tile (scatter) are never live
-  // at the same time, so they share one LDS buffer.
+  // Ranking words (one per sub-wave and digit: the sub-wave's running digit
+  // count in the high half, the match mask of the current item in the low
+  // half) and the staged tile (scatter) are never live at the same time, so
+  // they share one LDS buffer.
   constexpr size_t STAGE_BYTES = (TILE + 1) * STAGE_ELEM;
-  constexpr size_t MATCH_BYTES = size_t(WAVES) * NB * sizeof(uint64_t);
+  constexpr size_t RANK_BYTES = size_t(SUBS) * NB * sizeof(uint64_t);
   __shared__ __attribute__((aligned(16)))
-  unsigned char stage_raw[STAGE_BYTES > MATCH_BYTES ? STAGE_BYTES : MATCH_BYTES];
-  uint64_t(*match)[NB] = reinterpret_cast<uint64_t(*)[NB]>(stage_raw);
-  __shared__ uint32_t hist[WAVES][NB];
+  unsigned char stage_raw[STAGE_BYTES > RANK_BYTES ? STAGE_BYTES : RANK_BYTES];
+  uint64_t(*rankw)[NB] = reinterpret_cast<uint64_t(*)[NB]>(stage_raw);
+  // Per sub-wave and digit: first tile position of that sub-wave's keys.
+  __shared__ uint32_t hist[SUBS][NB];
   __shared__ uint32_t digit_off[BINS];
   __shared__ uint32_t wave_sum[BINS / 64];
   __shared__ uint32_t s_tile;
@@ -238,36 +282,38 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   Bits *stage_keys = reinterpret_cast<Bits *>(stage_raw);
 
   if (tid0 == 0) s_tile = add_agent(tile_counter, 1u);
-  for (uint32_t i = tid0; i < WAVES * NB; i += THREADS) (&hist[0][0])[i] = 0;
-  // Global start of each digit's bucket: exclusive scan of the pass's bins,
-  // the same for every tile, computed once.
-  uint32_t bin_start = 0;
-  {
-    const uint32_t lane = tid0 & 63u;
-    const uint32_t b = tid0 < BINS ? pass_bins[tid0] : 0u;
-    const uint32_t inc = wave_inclusive_sum(b, lane);
-    if (tid0 < BINS && lane == 63) wave_sum[tid0 >> 6] = inc;
-    __syncthreads();
-    if (tid0 < BINS) {
-      bin_start = inc - b;
-      for (uint32_t w = 0; w < (tid0 >> 6); ++w) bin_start += wave_sum[w];
-    }
-  }
-  uint32_t tile = s_tile;
+  // Global start of each digit's bucket (exclusive offsets computed by the
+  // histogram kernel).
+  const uint32_t bin_start = tid0 < BINS ? pass_bins[tid0] : 0u;
   __syncthreads();
+  uint32_t tile = s_tile;
   if (tile >= num_tiles) return;
-
-  // Wave-contiguous, lane-striped load: item j of lane l is key
-  // wave_base + 64 j + l, so (item, lane) order is source order.
+  // Sub-wave-contiguous, lane-striped load: item j of sub-wave lane l is key
+  // sub_base + 32 j + l, so (sub-wave, item, lane) order is source order.
+  // Loads are clamped instead of predicated: items past the end rank as
+  // dummies whatever they hold, and unpredicated loads keep the compiler's
+  // memory-counter waits exact.
   Bits key[ITEMS];
-  size_t wave_base = size_t(tile) * TILE + size_t(tid0 >> 6) * WAVE_ITEMS;
+  const size_t last_item = n - 1;
+  size_t sub_base = size_t(tile) * TILE + size_t(tid0 >> 5) * SUB_ITEMS;
 #pragma unroll
-  for (int j = 0; j < ITEMS; ++j) {
-    const size_t idx = wave_base + size_t(j) * 64 + (tid0 & 63u);
-    key[j] = idx < n ? keys_in[idx] : Bits(0);
-  }
+  for (int j = 0; j < ITEMS; ++j)
+    key[j] = keys_in[min(sub_base + size_t(j) * 32 + (tid0 & 31u), last_item)];
+  // The next tile is claimed one tile ahead by a thread of a wave that has no
+  // other global memory traffic before the claim is consumed, so waiting for
+  // the claim never waits for look-back or prefetch loads. Claims only ever
+  // grow, so a block's next tile is above its current one and the lowest
+  // tile in progress never waits on an unstarted tile.
+  constexpr uint32_t CLAIM = BINS;
+  static_assert(!RCCL_RADIX_PERSISTENT || THREADS > BINS,
+                "the claiming thread must not be a look-back thread");
+  uint32_t claimed = 0;
+
 
   while (true) {
+#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT == 0
+    if (threadIdx.x == CLAIM) claimed = add_agent(tile_counter, 1u);
+#endif
     // Values derived from the thread index are recomputed every tile: an
     // opaque copy keeps the compiler from hoisting dozens of per-item
     // addresses out of the tile loop into registers.
@@ -275,56 +321,57 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     asm volatile("" : "+v"(tid));
     const uint32_t lane = tid & 63u;
     const uint32_t wave = tid >> 6;
-    // The staging buffer of the previous tile becomes this tile's match
-    // masks: clear them (the end-of-tile barrier has passed).
-    for (uint32_t i = tid; i < WAVES * NB; i += THREADS) (&match[0][0])[i] = 0;
+    const uint32_t sw = tid >> 5;       // sub-wave
+    const uint32_t sl = tid & 31u;      // lane within the sub-wave
+    // The staging buffer of the previous tile becomes this tile's ranking
+    // words: clear them (the end-of-tile barrier has passed).
+    for (uint32_t i = tid; i < SUBS * NB; i += THREADS) (&rankw[0][0])[i] = 0;
     __syncthreads();
-    uint64_t *wmatch = match[wave];
-    uint32_t *whist = hist[wave];
-    const uint64_t lane_bit = 1ull << lane;
+    uint64_t *srank = rankw[sw];
+    const uint32_t lane_bit = 1u << sl;
     const size_t tile_base = size_t(tile) * TILE;
-    // Items of this wave's chunk that exist (the last tile may be partial).
-    const uint32_t wave_valid =
-        n > wave_base ? static_cast<uint32_t>(min<size_t>(n - wave_base, WAVE_ITEMS)) : 0u;
+    // Items of this sub-wave's chunk that exist (the last tile may be partial).
+    const uint32_t sub_valid =
+        n > sub_base ? static_cast<uint32_t>(min<size_t>(n - sub_base, SUB_ITEMS)) : 0u;
 
     ValReg val[ITEMS];
     if constexpr (PAIRS) {
       // Issued now, consumed after the key scatter.
 #pragma unroll
-      for (int j = 0; j < ITEMS; ++j) {
-        const uint32_t i = uint32_t(j) * 64 + lane;
-        val[j] = i < wave_valid ? vals_in[wave_base + i] : ValReg{};
-      }
+      for (int j = 0; j < ITEMS; ++j)
+        val[j] = vals_in[min(sub_base + size_t(j) * 32 + sl, last_item)];
     }
 
-    // Stable rank within the wave. For each item the lanes OR their lane bit
-    // into match[digit]; reading it back gives the peer set, whose popcount
-    // below this lane plus the wave's running digit count is the rank. The
-    // lowest peer advances the count and clears the mask for the next item.
-    // LDS operations of one wave execute in order, so no barrier is needed
-    // between the steps.
+    // Stable rank within the sub-wave. For each item the lanes OR their lane
+    // bit into the low half of their digit's ranking word; reading the word
+    // back gives the peer set and the sub-wave's running count for that digit
+    // in one load, and rank = count + peers below this lane. The lowest peer
+    // then writes count + peers with an empty mask, which both advances the
+    // count and clears the mask for the next item. LDS operations of one wave
+    // execute in order, so no barrier is needed between the steps.
     uint32_t rank[ITEMS];
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
       const uint32_t d =
-          uint32_t(j) * 64 + lane < wave_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
-      atomicOr(reinterpret_cast<unsigned long long *>(&wmatch[d]),
-               static_cast<unsigned long long>(lane_bit));
+          uint32_t(j) * 32 + sl < sub_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
+      atomicOr(reinterpret_cast<uint32_t *>(&srank[d]), lane_bit);
       __builtin_amdgcn_wave_barrier();
-      const uint64_t peers = wmatch[d];
-      const uint32_t base = whist[d];
-      const uint32_t below = popc_below(peers);
+      const uint64_t word = srank[d];
+      const uint32_t peers = static_cast<uint32_t>(word);
+      const uint32_t base = static_cast<uint32_t>(word >> 32);
+      const uint32_t below = static_cast<uint32_t>(__popc(peers & (lane_bit - 1u)));
       rank[j] = base + below;
       // Keep one register per item (not base and below separately).
       asm volatile("" : "+v"(rank[j]));
       __builtin_amdgcn_wave_barrier();
-      if (below == 0) {
-        whist[d] = base + static_cast<uint32_t>(__popcll(peers));
-        wmatch[d] = 0;
-      }
+      if (below == 0)
+        srank[d] = static_cast<uint64_t>(base + static_cast<uint32_t>(__popc(peers))) << 32;
       __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
+#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT == 1
+    if (tid == CLAIM) claimed = add_agent(tile_counter, 1u);
+#endif
 
     // Per digit: exclusive prefix over waves and tile total; publish the
     // aggregate and start the look-back loads at once.
@@ -337,8 +384,8 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     uint32_t ga[GWIN];
     if (tid < BINS) {
 #pragma unroll
-      for (int w = 0; w < WAVES; ++w) {
-        const uint32_t c = hist[w][tid];
+      for (int w = 0; w < SUBS; ++w) {
+        const uint32_t c = static_cast<uint32_t>(rankw[w][tid] >> 32);
         hist[w][tid] = count;
         count += c;
       }
@@ -347,59 +394,81 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
       add_agent(&lbuf.gagg[size_t(group) * BINS + tid], (1u << GAGG_SHIFT) | count);
       // Issue both first windows now: in-group predecessors (newest first)
       // and the groups before this one.
+      // Window loads are clamped to valid slots; slots outside the window
+      // are masked when the window is consumed, so the loads stay in flight
+      // until then.
 #pragma unroll
-      for (int w = 0; w < LOOKBACK; ++w) {
-        const int t = static_cast<int>(tile) - 1 - w;
-        lb[w] = t >= gfirst ? load_agent(&lbuf.tile[size_t(t) * BINS + tid]) : DI::BOUNDARY;
-      }
+      for (int w = 0; w < LOOKBACK; ++w)
+        lb[w] = load_agent(&lbuf.tile[size_t(max(static_cast<int>(tile) - 1 - w, 0)) * BINS + tid]);
 #pragma unroll
       for (int w = 0; w < GWIN; ++w) {
-        const int g = static_cast<int>(group) - 1 - w;
-        gi[w] = g >= 0 ? load_agent(&lbuf.ginc[size_t(g) * BINS + tid]) : DI::INCL;
-        ga[w] = g >= 0 ? load_agent(&lbuf.gagg[size_t(g) * BINS + tid]) : 0u;
+        const size_t g = size_t(max(static_cast<int>(group) - 1 - w, 0));
+        gi[w] = load_agent(&lbuf.ginc[g * BINS + tid]);
+        ga[w] = load_agent(&lbuf.gagg[g * BINS + tid]);
       }
       tile_inc = wave_inclusive_sum(count, lane);
       if (lane == 63) wave_sum[wave] = tile_inc;
     }
-    if (tid == 0) s_tile = add_agent(tile_counter, 1u);
     __syncthreads();
-    const uint32_t next = s_tile;
     uint32_t tile_start = 0;
     if (tid < BINS) {
       tile_start = tile_inc - count;
       for (uint32_t w = 0; w < wave; ++w) tile_start += wave_sum[w];
 #pragma unroll
-      for (int w = 0; w < WAVES; ++w) hist[w][tid] += tile_start;
+      for (int w = 0; w < SUBS; ++w) hist[w][tid] += tile_start;
     }
-    if (tid < WAVES) hist[tid][DUMMY] = TILE;  // dummy items stage into the spare slot
+    if (tid < SUBS) hist[tid][DUMMY] = TILE;  // dummy items stage into the spare slot
+#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT < 2
+    if (tid == CLAIM) s_tile = claimed;
+#endif
     __syncthreads();
+#if !RCCL_RADIX_PERSISTENT
+    const uint32_t next = num_tiles;
+#elif RCCL_RADIX_CLAIM_POINT < 2
+    const uint32_t next = s_tile;
+#else
+    if (tid == CLAIM) claimed = add_agent(tile_counter, 1u);
+#endif
 
     // Stage keys in digit order. The empty asm statements stop the compiler
     // from keeping per-item digit addresses alive from the ranking loop
     // (recomputing them is cheaper than the registers).
-    uint32_t slane = lane;
+    uint32_t slane = sl;
     asm volatile("" : "+v"(slane));
+    const uint32_t *shist = hist[sw];
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) asm volatile("" : "+v"(key[j]));
+    // In batches: the batch's offset reads are in flight together before its
+    // staging writes.
 #pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      const uint32_t d =
-          uint32_t(j) * 64 + slane < wave_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
-      rank[j] = min(rank[j] + whist[d], uint32_t(TILE));
-      stage_keys[rank[j]] = key[j];
-    }
-
-    // Prefetch the next tile's keys (the current keys are dead now); they
-    // land while this tile's look-back and scatter run.
-    Bits nkey[ITEMS];
-    const size_t next_wave_base = size_t(next) * TILE + size_t(wave) * WAVE_ITEMS;
-    if (next < num_tiles) {
+    for (int j0 = 0; j0 < ITEMS; j0 += BATCH) {
+      uint32_t base[BATCH];
 #pragma unroll
-      for (int j = 0; j < ITEMS; ++j) {
-        const size_t idx = next_wave_base + size_t(j) * 64 + lane;
-        nkey[j] = idx < n ? keys_in[idx] : Bits(0);
+      for (int b = 0; b < BATCH && j0 + b < ITEMS; ++b) {
+        const int j = j0 + b;
+        const uint32_t d =
+            uint32_t(j) * 32 + slane < sub_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
+        base[b] = shist[d];
+      }
+#pragma unroll
+      for (int b = 0; b < BATCH && j0 + b < ITEMS; ++b) {
+        const int j = j0 + b;
+        rank[j] = min(rank[j] + base[b], uint32_t(TILE));
+        stage_keys[rank[j]] = key[j];
       }
     }
+
+    // Prefetch the next tile's keys into the key registers (the current keys
+    // live in LDS now); they land while this tile's look-back and scatter
+    // run. No branch around the loads: past the last tile every element is
+    // masked off, and a fixed count of loads lets the look-back wait for its
+    // own window loads only.
+#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT < 2
+    const size_t next_sub_base = size_t(next) * TILE + size_t(sw) * SUB_ITEMS;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j)
+      key[j] = keys_in[min(next_sub_base + size_t(j) * 32 + sl, last_item)];
+#endif
 
     // Two-level decoupled look-back, one thread per digit, consuming the
     // windows issued above newest first. In-group predecessors are summed
@@ -409,58 +478,78 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     if (tid < BINS) {
       Desc excl = 0;
       bool done = tile == 0;
+      // Window slot w holds tile t - w; slots before the group are boundaries.
       int t = static_cast<int>(tile) - 1;
-      while (!done) {
+      auto eat_tiles = [&]() {
         int consumed = 0;
         bool stop = false;
 #pragma unroll
         for (int w = 0; w < LOOKBACK; ++w) {
           if (!done && !stop) {
-            const Desc flag = lb[w] >> DI::SHIFT;
+            const Desc v = t - w >= gfirst ? lb[w] : DI::BOUNDARY;
+            const Desc flag = v >> DI::SHIFT;
             if (flag == 0 || flag == (DI::BOUNDARY >> DI::SHIFT)) {
               stop = true;
             } else {
-              excl += lb[w] & DI::MASK;
+              excl += v & DI::MASK;
               ++consumed;
               done = flag == (DI::INCL >> DI::SHIFT);
             }
           }
         }
-        if (done) break;
         t -= consumed;
-        if (t < gfirst) break;  // every in-group predecessor summed
-        if (consumed == 0) __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-        for (int w = 0; w < LOOKBACK; ++w)
-          lb[w] = t - w >= gfirst ? load_agent(&lbuf.tile[size_t(t - w) * BINS + tid])
-                                  : DI::BOUNDARY;
-      }
+        return consumed;
+      };
+      // Group slot w holds group g - w; slots before group 0 read as an
+      // inclusive zero.
       int g = static_cast<int>(group) - 1;
-      while (!done) {
+      auto eat_groups = [&]() {
         int consumed = 0;
         bool blocked = false;
 #pragma unroll
         for (int w = 0; w < GWIN; ++w) {
           if (!done && !blocked) {
-            if ((gi[w] >> DI::SHIFT) == (DI::INCL >> DI::SHIFT)) {
-              excl += gi[w] & DI::MASK;
+            const bool real = g - w >= 0;
+            const Desc vi = real ? gi[w] : DI::INCL;
+            const uint32_t va = real ? ga[w] : 0u;
+            if ((vi >> DI::SHIFT) == (DI::INCL >> DI::SHIFT)) {
+              excl += vi & DI::MASK;
               done = true;
-            } else if ((ga[w] >> GAGG_SHIFT) == uint32_t(GROUP)) {
-              excl += ga[w] & GAGG_MASK;  // earlier groups are always full
+            } else if ((va >> GAGG_SHIFT) == uint32_t(GROUP)) {
+              excl += va & GAGG_MASK;  // earlier groups are always full
               ++consumed;
             } else {
               blocked = true;
             }
           }
         }
-        if (done) break;
         g -= consumed;
-        if (consumed == 0) __builtin_amdgcn_s_sleep(1);
+        return consumed;
+      };
+      // The first windows were issued before the staging; they are consumed
+      // outside the polling loops so that waiting for them does not wait for
+      // the prefetch issued after them.
+      if (!done) {
+        int c = eat_tiles();
+        while (!done && t >= gfirst) {
+          if (c == 0) __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-        for (int w = 0; w < GWIN; ++w) {
-          const int gg = g - w;
-          gi[w] = gg >= 0 ? load_agent(&lbuf.ginc[size_t(gg) * BINS + tid]) : DI::INCL;
-          ga[w] = gg >= 0 ? load_agent(&lbuf.gagg[size_t(gg) * BINS + tid]) : 0u;
+          for (int w = 0; w < LOOKBACK; ++w)
+            lb[w] = load_agent(&lbuf.tile[size_t(max(t - w, 0)) * BINS + tid]);
+          c = eat_tiles();
+        }
+      }
+      if (!done) {
+        int c = eat_groups();
+        while (!done) {
+          if (c == 0) __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+          for (int w = 0; w < GWIN; ++w) {
+            const size_t gg = size_t(max(g - w, 0));
+            gi[w] = load_agent(&lbuf.ginc[gg * BINS + tid]);
+            ga[w] = load_agent(&lbuf.gagg[gg * BINS + tid]);
+          }
+          c = eat_groups();
         }
       }
       const Desc incl = static_cast<Desc>(DI::INCL | (excl + Desc(count)));
@@ -469,9 +558,17 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
       if (tile == glast) store_agent(&lbuf.ginc[size_t(group) * BINS + tid], incl);
       digit_off[tid] = bin_start + static_cast<uint32_t>(excl) - tile_start;
     }
+#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT == 2
+    if (tid == CLAIM) s_tile = claimed;
+#endif
     __syncthreads();
-    // hist is free until the next tile's ranking: clear it now.
-    for (uint32_t i = tid; i < WAVES * NB; i += THREADS) (&hist[0][0])[i] = 0;
+#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT == 2
+    const uint32_t next = s_tile;
+    const size_t next_sub_base = size_t(next) * TILE + size_t(sw) * SUB_ITEMS;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j)
+      key[j] = keys_in[min(next_sub_base + size_t(j) * 32 + sl, last_item)];
+#endif
 
     // Coalesced scatter: consecutive staged keys of one digit go to
     // consecutive output positions.
@@ -479,26 +576,25 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     // Positions are exact when the bins match the keys; the clamp only keeps
     // a caller that changes the keys mid-sort from writing out of bounds.
     const uint32_t last = static_cast<uint32_t>(n - 1);
+    // In batches: the batch's staged keys are read together, then their
+    // digits' offsets together, then stored; only the stores are predicated.
     uint32_t dst[PAIRS ? ITEMS : 1];
-    if (valid_count == TILE) {
 #pragma unroll
-      for (int k = 0; k < ITEMS; ++k) {
-        const uint32_t i = uint32_t(k) * THREADS + tid;
-        const Bits kk = stage_keys[i];
-        const uint32_t p = min(digit_off[Ops::digit(kk, bit, mask)] + i, last);
-        keys_out[p] = kk;
-        if constexpr (PAIRS) dst[k] = p;
-      }
-    } else {
+    for (int k0 = 0; k0 < ITEMS; k0 += BATCH) {
+      Bits kk[BATCH];
+      uint32_t off[BATCH];
 #pragma unroll
-      for (int k = 0; k < ITEMS; ++k) {
-        const uint32_t i = uint32_t(k) * THREADS + tid;
-        if (i < valid_count) {
-          const Bits kk = stage_keys[i];
-          const uint32_t p = min(digit_off[Ops::digit(kk, bit, mask)] + i, last);
-          keys_out[p] = kk;
-          if constexpr (PAIRS) dst[k] = p;
-        }
+      for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b)
+        kk[b] = stage_keys[uint32_t(k0 + b) * THREADS + tid];
+#pragma unroll
+      for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b)
+        off[b] = digit_off[Ops::digit(kk[b], bit, mask)];
+#pragma unroll
+      for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b) {
+        const uint32_t i = uint32_t(k0 + b) * THREADS + tid;
+        const uint32_t p = min(off[b] + i, last);
+        if (i < valid_count) keys_out[p] = kk[b];
+        if constexpr (PAIRS) dst[k0 + b] = p;
       }
     }
     if constexpr (PAIRS) {
@@ -523,10 +619,10 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     __syncthreads();
 
     if (next >= num_tiles) break;
+#if RCCL_RADIX_PERSISTENT
     tile = next;
-    wave_base = next_wave_base;
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) key[j] = nkey[j];
+    sub_base = next_sub_base;
+#endif
   }
 }
 
@@ -591,6 +687,11 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
         reinterpret_cast<uint32_t *>(a.ws + l.lb[0]), zero_words);
   }
   RCCL_HIP_TRY(check_launch("radix histogram"));
+  {
+    KernelTimer t("radix_bins_scan", a.stream, passes * BINS);
+    bins_scan_kernel<<<1, BINS, 0, a.stream>>>(bins, passes);
+  }
+  RCCL_HIP_TRY(check_launch("radix bins scan"));
 
   // Persistent grid: as many blocks as fit on the device at once, but never
   // more than there are tiles.
@@ -608,8 +709,9 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
     if (blocks_per_cu < 1 || cus < 1)
       return set_error(RCCL_HIP_ERROR_LAUNCH, "radix onesweep does not fit on the device");
   }
-  const uint32_t grid =
-      static_cast<uint32_t>(std::min<size_t>(l.tiles, size_t(blocks_per_cu) * size_t(cus)));
+  const uint32_t grid = static_cast<uint32_t>(
+      RCCL_RADIX_PERSISTENT ? std::min<size_t>(l.tiles, size_t(blocks_per_cu) * size_t(cus))
+                            : l.tiles);
 
   for (uint32_t p = 0; p < passes; ++p) {
     const uint32_t bit = a.begin_bit + 8u * p;
