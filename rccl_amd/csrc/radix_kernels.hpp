@@ -85,20 +85,32 @@ template <class Desc> struct LookbackBuf {
 };
 
 // ---------------------------------------------------------------------------
-// Policy. Tile = THREADS x ITEMS keys; ITEMS depends on the widest staged
+// Policy. Tile = threads x items keys, the largest that keeps the staged tile
+// in LDS at full wave occupancy (per-tile costs, above all the look-back,
+// dominate smaller tiles). Keys-only sorts use two 512-thread blocks per CU;
+// pair sorts one 1024-thread block per CU. Items depend on the widest staged
 // element (key or value). Overridable at build time for tuning.
 // ---------------------------------------------------------------------------
-#ifndef RCCL_RADIX_THREADS
-#define RCCL_RADIX_THREADS 512
+#ifndef RCCL_RADIX_KEYS_THREADS
+#define RCCL_RADIX_KEYS_THREADS 512
 #endif
-#ifndef RCCL_RADIX_ITEMS_4B
-#define RCCL_RADIX_ITEMS_4B 24
+#ifndef RCCL_RADIX_KEYS_ITEMS_4B
+#define RCCL_RADIX_KEYS_ITEMS_4B 34
 #endif
-#ifndef RCCL_RADIX_ITEMS_8B
-#define RCCL_RADIX_ITEMS_8B 12
+#ifndef RCCL_RADIX_KEYS_ITEMS_8B
+#define RCCL_RADIX_KEYS_ITEMS_8B 17
 #endif
-#ifndef RCCL_RADIX_ITEMS_16B
-#define RCCL_RADIX_ITEMS_16B 7
+#ifndef RCCL_RADIX_PAIRS_THREADS
+#define RCCL_RADIX_PAIRS_THREADS 1024
+#endif
+#ifndef RCCL_RADIX_PAIRS_ITEMS_4B
+#define RCCL_RADIX_PAIRS_ITEMS_4B 28
+#endif
+#ifndef RCCL_RADIX_PAIRS_ITEMS_8B
+#define RCCL_RADIX_PAIRS_ITEMS_8B 14
+#endif
+#ifndef RCCL_RADIX_PAIRS_ITEMS_16B
+#define RCCL_RADIX_PAIRS_ITEMS_16B 7
 #endif
 #ifndef RCCL_RADIX_LOOKBACK_WINDOW
 #define RCCL_RADIX_LOOKBACK_WINDOW 16
@@ -126,20 +138,26 @@ template <class Desc> struct LookbackBuf {
 #ifndef RCCL_RADIX_GROUP_WINDOW
 #define RCCL_RADIX_GROUP_WINDOW 4
 #endif
-constexpr int THREADS = RCCL_RADIX_THREADS;
 constexpr int LOOKBACK = RCCL_RADIX_LOOKBACK_WINDOW;
 constexpr int GROUP = RCCL_RADIX_LOOKBACK_GROUP;
 constexpr int GWIN = RCCL_RADIX_GROUP_WINDOW;
 
-constexpr int items_for(size_t elem_bytes) {
-  return elem_bytes <= 4 ? RCCL_RADIX_ITEMS_4B
-                         : (elem_bytes <= 8 ? RCCL_RADIX_ITEMS_8B : RCCL_RADIX_ITEMS_16B);
+constexpr int threads_for(size_t value_bytes) {
+  return value_bytes ? RCCL_RADIX_PAIRS_THREADS : RCCL_RADIX_KEYS_THREADS;
 }
 constexpr size_t stage_elem(size_t key_bytes, size_t value_bytes) {
   return key_bytes > value_bytes ? key_bytes : value_bytes;
 }
-inline size_t tile_items(size_t key_bytes, size_t value_bytes) {
-  return size_t(THREADS) * items_for(stage_elem(key_bytes, value_bytes));
+constexpr int items_for(size_t key_bytes, size_t value_bytes) {
+  return value_bytes == 0
+             ? (key_bytes <= 4 ? RCCL_RADIX_KEYS_ITEMS_4B : RCCL_RADIX_KEYS_ITEMS_8B)
+             : (stage_elem(key_bytes, value_bytes) <= 4
+                    ? RCCL_RADIX_PAIRS_ITEMS_4B
+                    : (stage_elem(key_bytes, value_bytes) <= 8 ? RCCL_RADIX_PAIRS_ITEMS_8B
+                                                               : RCCL_RADIX_PAIRS_ITEMS_16B));
+}
+constexpr size_t tile_items(size_t key_bytes, size_t value_bytes) {
+  return size_t(threads_for(value_bytes)) * items_for(key_bytes, value_bytes);
 }
 
 // ---------------------------------------------------------------------------
@@ -235,7 +253,7 @@ __global__ void __launch_bounds__(BINS) bins_scan_kernel(uint32_t *bins, uint32_
 // is published, and the keys of the next tile are loaded before t's
 // look-back is consumed.
 // ---------------------------------------------------------------------------
-template <class Bits, class Val, class Ops, int ITEMS, class Desc>
+template <class Bits, class Val, class Ops, int ITEMS, class Desc, int THREADS>
 __global__ void __launch_bounds__(THREADS, RCCL_RADIX_WAVES_PER_SIMD)
 onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
                 const Val *__restrict__ vals_in, Val *__restrict__ vals_out, size_t n,
@@ -273,7 +291,9 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   unsigned char stage_raw[STAGE_BYTES > RANK_BYTES ? STAGE_BYTES : RANK_BYTES];
   uint64_t(*rankw)[NB] = reinterpret_cast<uint64_t(*)[NB]>(stage_raw);
   // Per sub-wave and digit: first tile position of that sub-wave's keys.
-  __shared__ uint32_t hist[SUBS][NB];
+  // 16-bit: offsets are tile-relative (at most TILE), which halves the table.
+  static_assert(TILE < 65536, "tile offsets are 16-bit");
+  __shared__ uint16_t hist[SUBS][NB];
   __shared__ uint32_t digit_off[BINS];
   __shared__ uint32_t wave_sum[BINS / 64];
   __shared__ uint32_t s_tile;
@@ -386,7 +406,7 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
 #pragma unroll
       for (int w = 0; w < SUBS; ++w) {
         const uint32_t c = static_cast<uint32_t>(rankw[w][tid] >> 32);
-        hist[w][tid] = count;
+        hist[w][tid] = static_cast<uint16_t>(count);
         count += c;
       }
       store_agent(&lbuf.tile[size_t(tile) * BINS + tid],
@@ -415,7 +435,7 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
       tile_start = tile_inc - count;
       for (uint32_t w = 0; w < wave; ++w) tile_start += wave_sum[w];
 #pragma unroll
-      for (int w = 0; w < SUBS; ++w) hist[w][tid] += tile_start;
+      for (int w = 0; w < SUBS; ++w) hist[w][tid] = static_cast<uint16_t>(hist[w][tid] + tile_start);
     }
     if (tid < SUBS) hist[tid][DUMMY] = TILE;  // dummy items stage into the spare slot
 #if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT < 2
@@ -435,7 +455,7 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     // (recomputing them is cheaper than the registers).
     uint32_t slane = sl;
     asm volatile("" : "+v"(slane));
-    const uint32_t *shist = hist[sw];
+    const uint16_t *shist = hist[sw];
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) asm volatile("" : "+v"(key[j]));
     // In batches: the batch's offset reads are in flight together before its
@@ -658,8 +678,9 @@ struct SortArgs {
 
 template <class Bits, class Val, class Ops, class Desc>
 rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
-  constexpr int ITEMS =
-      items_for(stage_elem(sizeof(Bits), std::is_same<Val, NoValue>::value ? 0 : sizeof(Val)));
+  constexpr size_t VBYTES = std::is_same<Val, NoValue>::value ? 0 : sizeof(Val);
+  constexpr int ITEMS = items_for(sizeof(Bits), VBYTES);
+  constexpr int THREADS = threads_for(VBYTES);
   uint32_t *bins = reinterpret_cast<uint32_t *>(a.ws + l.bins);
   uint32_t *counters = reinterpret_cast<uint32_t *>(a.ws + l.counters);
   LookbackBuf<Desc> lb[2];
@@ -704,7 +725,7 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
       err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (err == hipSuccess)
       err = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &blocks_per_cu, onesweep_kernel<Bits, Val, Ops, ITEMS, Desc>, THREADS, 0);
+          &blocks_per_cu, onesweep_kernel<Bits, Val, Ops, ITEMS, Desc, THREADS>, THREADS, 0);
     if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "radix occupancy", err);
     if (blocks_per_cu < 1 || cus < 1)
       return set_error(RCCL_HIP_ERROR_LAUNCH, "radix onesweep does not fit on the device");
@@ -719,7 +740,7 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
     const uint32_t mask = (1u << width) - 1u;
     const int in = a.cur, out = 1 - a.cur;
     KernelTimer t("radix_onesweep", a.stream, a.n);
-    onesweep_kernel<Bits, Val, Ops, ITEMS, Desc><<<dim3(grid), THREADS, 0, a.stream>>>(
+    onesweep_kernel<Bits, Val, Ops, ITEMS, Desc, THREADS><<<dim3(grid), THREADS, 0, a.stream>>>(
         static_cast<const Bits *>(a.keys[in]), static_cast<Bits *>(a.keys[out]),
         static_cast<const Val *>(a.vals[in]), static_cast<Val *>(a.vals[out]), a.n,
         static_cast<uint32_t>(l.tiles), bins + size_t(p) * BINS, lb[p & 1],
