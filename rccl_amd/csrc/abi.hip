@@ -7,6 +7,12 @@
 #include "common.hpp"
 
 namespace rccl_hip {
+namespace radix {
+rccl_hip_status check_lane_order();
+} // namespace radix
+} // namespace rccl_hip
+
+namespace rccl_hip {
 
 namespace {
 struct TimingRecord {
@@ -134,6 +140,22 @@ rccl_hip_status rccl_hip_program_load(int device) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0 ||
       (prop.gcnArchName[6] != '\0' && prop.gcnArchName[6] != ':'))
     return rccl_hip::set_error(RCCL_HIP_ERROR_UNSUPPORTED_TARGET, "gfx950 kernels");
+  // The radix ranking relies on lane-ordered LDS atomics: verify once per
+  // device, on that device.
+  static std::mutex mu;
+  static std::vector<int> checked;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int d : checked)
+    if (d == device) return rccl_hip::ok();
+  int current = 0;
+  err = hipGetDevice(&current);
+  if (err == hipSuccess) err = hipSetDevice(device);
+  if (err != hipSuccess) return rccl_hip::set_hip_error(RCCL_HIP_ERROR_DRIVER, "set device", err);
+  const rccl_hip_status st = rccl_hip::radix::check_lane_order();
+  err = hipSetDevice(current);
+  if (st != RCCL_HIP_SUCCESS) return st;
+  if (err != hipSuccess) return rccl_hip::set_hip_error(RCCL_HIP_ERROR_DRIVER, "set device", err);
+  checked.push_back(device);
   return rccl_hip::ok();
 }
 

@@ -16,8 +16,6 @@ Layout layout(size_t key_bytes, size_t value_bytes, size_t n) {
   size_t off = 0;
   l.bins = off;
   off += align_up(max_passes * BINS * sizeof(uint32_t), 256);
-  l.counters = off;
-  off += align_up(max_passes * sizeof(uint32_t), 256);
   l.groups = (l.tiles + GROUP - 1) / GROUP;
   l.lb_ginc = align_up(l.tiles * BINS * l.desc_bytes, 256);
   l.lb_gagg = l.lb_ginc + align_up(l.groups * BINS * l.desc_bytes, 256);
@@ -28,6 +26,66 @@ Layout layout(size_t key_bytes, size_t value_bytes, size_t n) {
   off += l.lb_bytes;
   l.total = n == 0 ? 0 : off;
   return l;
+}
+
+namespace {
+
+// Lane-order self-check (see the onesweep notes): each wave repeatedly adds 1
+// to per-wave LDS counters chosen by a hash of (round, lane) restricted to
+// 1, 2, 16 or 256 counters, and checks that lanes hitting the same counter
+// received consecutive values in lane order. One block of CHECK_THREADS;
+// violations are counted into *bad.
+constexpr int CHECK_THREADS = 256;
+__global__ void __launch_bounds__(CHECK_THREADS) lane_order_check_kernel(uint32_t *bad) {
+  __shared__ uint32_t c[CHECK_THREADS / 64][BINS];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  for (uint32_t i = tid; i < (CHECK_THREADS / 64) * BINS; i += CHECK_THREADS) (&c[0][0])[i] = 0;
+  __syncthreads();
+  uint32_t nbad = 0;
+  for (uint32_t round = 0; round < 64; ++round) {
+    uint32_t h = (round * 0x9e3779b9u) ^ (tid * 0x85ebca6bu);
+    h ^= h >> 15;
+    h *= 0x2c1b3c6du;
+    h ^= h >> 12;
+    const uint32_t mask = round % 4 == 0 ? 0u : round % 4 == 1 ? 1u : round % 4 == 2 ? 15u : 255u;
+    const uint32_t d = h & mask;
+    const uint32_t got =
+        __hip_atomic_fetch_add(&c[wave][d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    // Lanes below with the same counter, and the lowest such lane.
+    uint32_t below = 0, first = lane;
+    for (int l = 63; l >= 0; --l) {
+      const uint32_t dl = static_cast<uint32_t>(__shfl(static_cast<int>(d), l, 64));
+      if (dl == d && static_cast<uint32_t>(l) < lane) {
+        ++below;
+        first = static_cast<uint32_t>(l);
+      }
+    }
+    const uint32_t base = got - below;
+    nbad += static_cast<uint32_t>(__shfl(static_cast<int>(base), static_cast<int>(first), 64)) !=
+            base;
+  }
+  if (nbad) atomicAdd(bad, nbad);
+}
+
+} // namespace
+
+rccl_hip_status check_lane_order() {
+  uint32_t *bad = nullptr;
+  hipError_t err = hipMalloc(&bad, sizeof(uint32_t));
+  if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_MEMORY, "lane-order check", err);
+  uint32_t host = 0;
+  err = hipMemset(bad, 0, sizeof(uint32_t));
+  if (err == hipSuccess) {
+    lane_order_check_kernel<<<1, CHECK_THREADS>>>(bad);
+    err = hipGetLastError();
+  }
+  if (err == hipSuccess) err = hipMemcpy(&host, bad, sizeof(uint32_t), hipMemcpyDeviceToHost);
+  const hipError_t free_err = hipFree(bad);
+  if (err == hipSuccess) err = free_err;
+  if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "lane-order check", err);
+  if (host != 0)
+    return set_error(RCCL_HIP_ERROR_UNSUPPORTED_TARGET, "lane-ordered LDS atomics", 0, host);
+  return ok();
 }
 
 namespace {

@@ -3,14 +3,15 @@
 // Reference behaviour: rccl-cub/src/radix.rs:364-876 (validation and pass
 // control) and rccl-cub/src/ordering_backend/radix.rs (device agents). The
 // kernels are an independent wave64 design:
-//   init        zero the per-pass bins and tile counters (one tiny block)
+//   init        zero the per-pass bins (one tiny block)
 //   histogram   one read of all keys builds every pass's 256-bin histogram in
 //               LDS (per-wave private counters) and adds them to the bins; it
 //               also zeroes look-back buffer 0
-//   onesweep    one launch per pass; persistent blocks claim tiles in order,
-//               rank them with wave64 LDS match masks, run a windowed
-//               decoupled look-back on agent-scope atomics, and scatter
-//               through LDS so HBM writes coalesce
+//   onesweep    one launch per pass, one tile per block (XCD-aware tile
+//               order); per-wave LDS digit counts, ranking by lane-ordered
+//               returning LDS atomics, a windowed two-level decoupled
+//               look-back on agent-scope atomics, and a scatter through LDS
+//               so HBM writes coalesce
 #pragma once
 
 #include <algorithm>
@@ -121,26 +122,22 @@ template <class Desc> struct LookbackBuf {
 #ifndef RCCL_RADIX_LOOKBACK_GROUP
 #define RCCL_RADIX_LOOKBACK_GROUP 16
 #endif
-// Where the next tile is claimed: 0 at the start of a tile, 1 after its
-// ranking, 2 at its staging (the prefetch of the next tile's keys then
-// follows the look-back).
-#ifndef RCCL_RADIX_CLAIM_POINT
-#define RCCL_RADIX_CLAIM_POINT 1
-#endif
-// 1: a persistent grid whose blocks loop over tiles, claiming the next tile
-// one ahead and prefetching its keys; 0: one tile per block.
-#ifndef RCCL_RADIX_PERSISTENT
-#define RCCL_RADIX_PERSISTENT 0
-#endif
 #ifndef RCCL_RADIX_LDS_BATCH
 #define RCCL_RADIX_LDS_BATCH 8
 #endif
 #ifndef RCCL_RADIX_GROUP_WINDOW
 #define RCCL_RADIX_GROUP_WINDOW 4
 #endif
+// Tiles per XCD run: consecutive tiles are handed to consecutive blocks of one
+// XCD in runs of this many (see onesweep_kernel).
+#ifndef RCCL_RADIX_XCD_RUN
+#define RCCL_RADIX_XCD_RUN 8
+#endif
 constexpr int LOOKBACK = RCCL_RADIX_LOOKBACK_WINDOW;
 constexpr int GROUP = RCCL_RADIX_LOOKBACK_GROUP;
 constexpr int GWIN = RCCL_RADIX_GROUP_WINDOW;
+constexpr uint32_t XCDS = 8;  // gfx950: 8 XCDs, blocks placed round-robin
+constexpr uint32_t XCD_RUN = RCCL_RADIX_XCD_RUN;
 
 constexpr int threads_for(size_t value_bytes) {
   return value_bytes ? RCCL_RADIX_PAIRS_THREADS : RCCL_RADIX_KEYS_THREADS;
@@ -161,14 +158,12 @@ constexpr size_t tile_items(size_t key_bytes, size_t value_bytes) {
 }
 
 // ---------------------------------------------------------------------------
-// init: zero bins and tile counters. (Internal linkage: every translation
-// unit that launches it carries its own copy.)
+// init: zero the bins. (Internal linkage: every translation unit that
+// launches it carries its own copy.)
 // ---------------------------------------------------------------------------
 namespace {
-__global__ void __launch_bounds__(256) init_kernel(uint32_t *bins, uint32_t *counters,
-                                                   uint32_t passes) {
+__global__ void __launch_bounds__(256) init_kernel(uint32_t *bins, uint32_t passes) {
   for (uint32_t i = threadIdx.x; i < passes * BINS; i += 256) bins[i] = 0;
-  if (threadIdx.x < passes) counters[threadIdx.x] = 0;
 }
 } // namespace
 
@@ -247,402 +242,351 @@ __global__ void __launch_bounds__(BINS) bins_scan_kernel(uint32_t *bins, uint32_
 } // namespace
 
 // ---------------------------------------------------------------------------
-// onesweep: one stable counting-sort pass. Persistent blocks claim tiles of
-// THREADS*ITEMS keys in order from an atomic counter and software-pipeline
-// them: the look-back window for tile t is issued right after t's aggregate
-// is published, and the keys of the next tile are loaded before t's
-// look-back is consumed.
+// onesweep: one stable counting-sort pass, one tile per block.
+//
+// Per tile: load the keys (wave-contiguous, lane-striped), count digits into
+// per-wave LDS counters, publish the tile's digit counts for the look-back,
+// turn the counters into tile positions, rank every key with one returning
+// LDS atomic, stage the tile in digit order, finish the look-back and scatter
+// so that each digit's keys leave in contiguous runs.
+//
+// Ranking relies on a property of the gfx950 LDS: lanes of one atomic
+// instruction that hit the same address are served in ascending lane order,
+// so the returned counter values of equal digits follow the lane order. The
+// library checks this once per device at load time (lane_order_check_kernel)
+// and refuses to run where it does not hold.
 // ---------------------------------------------------------------------------
+
+// s_waitcnt vmcnt(N): wait until at most N vector memory operations of this
+// wave are outstanding (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt
+// and lgkmcnt left at their no-wait maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier that orders LDS only: global loads and stores issued
+// before it stay in flight (__syncthreads would wait for all of them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Tile processed by a block. Blocks are placed on the XCDs round-robin
+// (block b on XCD b % 8), so giving runs of XCD_RUN consecutive tiles to
+// consecutive blocks of one XCD makes neighbouring tiles share an L2: the
+// cache lines they both write at digit-run boundaries are merged there
+// instead of reaching HBM as two partial writes. Every tile's predecessor
+// belongs to a block at most 8 * XCD_RUN - 9 indices later, far fewer than
+// the blocks resident at once, so in-order dispatch guarantees that the tile a
+// look-back waits on has been started.
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t block) {
+  const uint32_t x = block % XCDS, j = block / XCDS;
+  return XCDS * XCD_RUN * (j / XCD_RUN) + XCD_RUN * x + j % XCD_RUN;
+}
+inline size_t onesweep_grid(size_t tiles) {
+  const size_t row = size_t(XCDS) * XCD_RUN;
+  return (tiles + row - 1) / row * row;
+}
+
+// Two-level decoupled look-back for one digit (one thread per digit): in-group
+// predecessors tile by tile until an inclusive prefix or the group start, then
+// earlier groups whole (complete aggregates) until a group's inclusive prefix.
+// lb, gi and ga hold the first windows, issued when the tile's own counts were
+// published; a slot not yet published is polled again. Returns the exclusive
+// prefix of the tile's count for this digit.
+template <class Desc>
+__device__ __forceinline__ Desc lookback_consume(const LookbackBuf<Desc> &lbuf, uint32_t tile,
+                                                 uint32_t group, uint32_t digit,
+                                                 Desc (&lb)[LOOKBACK], Desc (&gi)[GWIN],
+                                                 uint32_t (&ga)[GWIN]) {
+  using DI = DescInfo<Desc>;
+  const int gfirst = static_cast<int>(group) * GROUP;
+  Desc excl = 0;
+  bool done = tile == 0;
+  // Window slot w holds tile t - w; slots before the group are boundaries.
+  int t = static_cast<int>(tile) - 1;
+  auto eat_tiles = [&]() {
+    int consumed = 0;
+    bool stop = false;
+#pragma unroll
+    for (int w = 0; w < LOOKBACK; ++w) {
+      if (!done && !stop) {
+        const Desc v = t - w >= gfirst ? lb[w] : DI::BOUNDARY;
+        const Desc flag = v >> DI::SHIFT;
+        if (flag == 0 || flag == (DI::BOUNDARY >> DI::SHIFT)) {
+          stop = true;
+        } else {
+          excl += v & DI::MASK;
+          ++consumed;
+          done = flag == (DI::INCL >> DI::SHIFT);
+        }
+      }
+    }
+    t -= consumed;
+    return consumed;
+  };
+  // Group slot w holds group g - w; slots before group 0 read as an inclusive
+  // zero.
+  int g = static_cast<int>(group) - 1;
+  auto eat_groups = [&]() {
+    int consumed = 0;
+    bool blocked = false;
+#pragma unroll
+    for (int w = 0; w < GWIN; ++w) {
+      if (!done && !blocked) {
+        const bool real = g - w >= 0;
+        const Desc vi = real ? gi[w] : DI::INCL;
+        const uint32_t va = real ? ga[w] : 0u;
+        if ((vi >> DI::SHIFT) == (DI::INCL >> DI::SHIFT)) {
+          excl += vi & DI::MASK;
+          done = true;
+        } else if ((va >> GAGG_SHIFT) == uint32_t(GROUP)) {
+          excl += va & GAGG_MASK;  // earlier groups are always full
+          ++consumed;
+        } else {
+          blocked = true;
+        }
+      }
+    }
+    g -= consumed;
+    return consumed;
+  };
+  if (!done) {
+    int c = eat_tiles();
+    while (!done && t >= gfirst) {
+      if (c == 0) __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int w = 0; w < LOOKBACK; ++w)
+        lb[w] = load_agent(&lbuf.tile[size_t(max(t - w, 0)) * BINS + digit]);
+      c = eat_tiles();
+    }
+  }
+  if (!done) {
+    int c = eat_groups();
+    while (!done) {
+      if (c == 0) __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int w = 0; w < GWIN; ++w) {
+        const size_t gg = size_t(max(g - w, 0));
+        gi[w] = load_agent(&lbuf.ginc[gg * BINS + digit]);
+        ga[w] = load_agent(&lbuf.gagg[gg * BINS + digit]);
+      }
+      c = eat_groups();
+    }
+  }
+  return excl;
+}
+
 template <class Bits, class Val, class Ops, int ITEMS, class Desc, int THREADS>
 __global__ void __launch_bounds__(THREADS, RCCL_RADIX_WAVES_PER_SIMD)
 onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
                 const Val *__restrict__ vals_in, Val *__restrict__ vals_out, size_t n,
                 uint32_t num_tiles, const uint32_t *__restrict__ pass_bins,
-                LookbackBuf<Desc> lbuf, LookbackBuf<Desc> lbuf_next, uint32_t *tile_counter,
-                uint32_t bit, uint32_t mask) {
+                LookbackBuf<Desc> lbuf, LookbackBuf<Desc> lbuf_next, uint32_t bit,
+                uint32_t mask) {
   constexpr bool PAIRS = !std::is_same<Val, NoValue>::value;
   constexpr int WAVES = THREADS / 64;
-  // Ranking works on 32-lane halves of each wave ("sub-waves"), each owning a
-  // contiguous chunk of 32 * ITEMS keys.
-  constexpr int SUBS = 2 * WAVES;
   constexpr int TILE = THREADS * ITEMS;
-  constexpr int SUB_ITEMS = 32 * ITEMS;
-  // LDS reads issued back to back before their results are used.
-  constexpr int BATCH = RCCL_RADIX_LDS_BATCH;
-  // Items past the end of the input (last tile only) rank in an extra
-  // dummy bin and stage into one spare slot, so the loops need no branches.
+  constexpr int WAVE_ITEMS = 64 * ITEMS;
+  // Items past the end of the input (last tile only) count in an extra dummy
+  // bin and stage into one spare slot, so the loops need no branches.
   constexpr int NB = BINS + 1;
   constexpr uint32_t DUMMY = BINS;
   constexpr size_t VAL_BYTES = PAIRS ? sizeof(Val) : 0;
   constexpr size_t STAGE_ELEM = sizeof(Bits) > VAL_BYTES ? sizeof(Bits) : VAL_BYTES;
+  constexpr int BATCH = RCCL_RADIX_LDS_BATCH;
   static_assert(THREADS >= BINS, "one thread per digit is required");
   static_assert(uint64_t(GROUP) * TILE <= GAGG_MASK, "group counts must fit the packed word");
   static_assert(LOOKBACK >= 1 && GWIN >= 1, "look-back windows");
   using DI = DescInfo<Desc>;
   using ValReg = typename std::conditional<PAIRS, Val, char>::type;
 
-  // Ranking words (one per sub-wave and digit: the sub-wave's running digit
-  // count in the high half, the match mask of the current item in the low
-  // half) and the staged tile (scatter) are never live at the same time, so
-  // they share one LDS buffer.
-  constexpr size_t STAGE_BYTES = (TILE + 1) * STAGE_ELEM;
-  constexpr size_t RANK_BYTES = size_t(SUBS) * NB * sizeof(uint64_t);
-  __shared__ __attribute__((aligned(16)))
-  unsigned char stage_raw[STAGE_BYTES > RANK_BYTES ? STAGE_BYTES : RANK_BYTES];
-  uint64_t(*rankw)[NB] = reinterpret_cast<uint64_t(*)[NB]>(stage_raw);
-  // Per sub-wave and digit: first tile position of that sub-wave's keys.
-  // 16-bit: offsets are tile-relative (at most TILE), which halves the table.
-  static_assert(TILE < 65536, "tile offsets are 16-bit");
-  __shared__ uint16_t hist[SUBS][NB];
+  __shared__ __attribute__((aligned(16))) unsigned char stage_raw[(TILE + 1) * STAGE_ELEM];
+  __shared__ uint32_t cnt[WAVES][NB];  // per-wave digit counters, then positions
   __shared__ uint32_t digit_off[BINS];
   __shared__ uint32_t wave_sum[BINS / 64];
-  __shared__ uint32_t s_tile;
-
-  const uint32_t tid0 = threadIdx.x;
   Bits *stage_keys = reinterpret_cast<Bits *>(stage_raw);
 
-  if (tid0 == 0) s_tile = add_agent(tile_counter, 1u);
-  // Global start of each digit's bucket (exclusive offsets computed by the
-  // histogram kernel).
-  const uint32_t bin_start = tid0 < BINS ? pass_bins[tid0] : 0u;
-  __syncthreads();
-  uint32_t tile = s_tile;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave = tid >> 6;
+  const uint32_t tile = xcd_tile(blockIdx.x);
   if (tile >= num_tiles) return;
-  // Sub-wave-contiguous, lane-striped load: item j of sub-wave lane l is key
-  // sub_base + 32 j + l, so (sub-wave, item, lane) order is source order.
-  // Loads are clamped instead of predicated: items past the end rank as
-  // dummies whatever they hold, and unpredicated loads keep the compiler's
-  // memory-counter waits exact.
-  Bits key[ITEMS];
+  for (uint32_t i = tid; i < WAVES * NB; i += THREADS) (&cnt[0][0])[i] = 0;
+  // Global start of each digit's bucket (exclusive offsets from bins_scan).
+  const uint32_t bin_start = tid < BINS ? pass_bins[tid] : 0u;
+
+  // Wave-contiguous, lane-striped load: item j of lane l is key
+  // wave_base + 64 j + l, so (wave, item, lane) order is source order. Loads
+  // are clamped instead of predicated; items past the end rank as dummies
+  // whatever they hold.
   const size_t last_item = n - 1;
-  size_t sub_base = size_t(tile) * TILE + size_t(tid0 >> 5) * SUB_ITEMS;
+  const size_t wave_base = size_t(tile) * TILE + size_t(wave) * WAVE_ITEMS;
+  Bits key[ITEMS];
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j)
-    key[j] = keys_in[min(sub_base + size_t(j) * 32 + (tid0 & 31u), last_item)];
-  // The next tile is claimed one tile ahead by a thread of a wave that has no
-  // other global memory traffic before the claim is consumed, so waiting for
-  // the claim never waits for look-back or prefetch loads. Claims only ever
-  // grow, so a block's next tile is above its current one and the lowest
-  // tile in progress never waits on an unstarted tile.
-  constexpr uint32_t CLAIM = BINS;
-  static_assert(!RCCL_RADIX_PERSISTENT || THREADS > BINS,
-                "the claiming thread must not be a look-back thread");
-  uint32_t claimed = 0;
-
-
-  while (true) {
-#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT == 0
-    if (threadIdx.x == CLAIM) claimed = add_agent(tile_counter, 1u);
-#endif
-    // Values derived from the thread index are recomputed every tile: an
-    // opaque copy keeps the compiler from hoisting dozens of per-item
-    // addresses out of the tile loop into registers.
-    uint32_t tid = tid0;
-    asm volatile("" : "+v"(tid));
-    const uint32_t lane = tid & 63u;
-    const uint32_t wave = tid >> 6;
-    const uint32_t sw = tid >> 5;       // sub-wave
-    const uint32_t sl = tid & 31u;      // lane within the sub-wave
-    // The staging buffer of the previous tile becomes this tile's ranking
-    // words: clear them (the end-of-tile barrier has passed).
-    for (uint32_t i = tid; i < SUBS * NB; i += THREADS) (&rankw[0][0])[i] = 0;
-    __syncthreads();
-    uint64_t *srank = rankw[sw];
-    const uint32_t lane_bit = 1u << sl;
-    const size_t tile_base = size_t(tile) * TILE;
-    // Items of this sub-wave's chunk that exist (the last tile may be partial).
-    const uint32_t sub_valid =
-        n > sub_base ? static_cast<uint32_t>(min<size_t>(n - sub_base, SUB_ITEMS)) : 0u;
-
-    ValReg val[ITEMS];
-    if constexpr (PAIRS) {
-      // Issued now, consumed after the key scatter.
-#pragma unroll
-      for (int j = 0; j < ITEMS; ++j)
-        val[j] = vals_in[min(sub_base + size_t(j) * 32 + sl, last_item)];
-    }
-
-    // Stable rank within the sub-wave. For each item the lanes OR their lane
-    // bit into the low half of their digit's ranking word; reading the word
-    // back gives the peer set and the sub-wave's running count for that digit
-    // in one load, and rank = count + peers below this lane. The lowest peer
-    // then writes count + peers with an empty mask, which both advances the
-    // count and clears the mask for the next item. LDS operations of one wave
-    // execute in order, so no barrier is needed between the steps.
-    uint32_t rank[ITEMS];
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      const uint32_t d =
-          uint32_t(j) * 32 + sl < sub_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
-      atomicOr(reinterpret_cast<uint32_t *>(&srank[d]), lane_bit);
-      __builtin_amdgcn_wave_barrier();
-      const uint64_t word = srank[d];
-      const uint32_t peers = static_cast<uint32_t>(word);
-      const uint32_t base = static_cast<uint32_t>(word >> 32);
-      const uint32_t below = static_cast<uint32_t>(__popc(peers & (lane_bit - 1u)));
-      rank[j] = base + below;
-      // Keep one register per item (not base and below separately).
-      asm volatile("" : "+v"(rank[j]));
-      __builtin_amdgcn_wave_barrier();
-      if (below == 0)
-        srank[d] = static_cast<uint64_t>(base + static_cast<uint32_t>(__popc(peers))) << 32;
-      __builtin_amdgcn_wave_barrier();
-    }
-    __syncthreads();
-#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT == 1
-    if (tid == CLAIM) claimed = add_agent(tile_counter, 1u);
-#endif
-
-    // Per digit: exclusive prefix over waves and tile total; publish the
-    // aggregate and start the look-back loads at once.
-    uint32_t count = 0;
-    uint32_t tile_inc = 0;
-    const uint32_t group = tile / GROUP;
-    const int gfirst = static_cast<int>(group) * GROUP;
-    Desc lb[LOOKBACK];
-    Desc gi[GWIN];
-    uint32_t ga[GWIN];
-    if (tid < BINS) {
-#pragma unroll
-      for (int w = 0; w < SUBS; ++w) {
-        const uint32_t c = static_cast<uint32_t>(rankw[w][tid] >> 32);
-        hist[w][tid] = static_cast<uint16_t>(count);
-        count += c;
-      }
-      store_agent(&lbuf.tile[size_t(tile) * BINS + tid],
-                  static_cast<Desc>((tile == 0 ? DI::INCL : DI::AGG) | Desc(count)));
-      add_agent(&lbuf.gagg[size_t(group) * BINS + tid], (1u << GAGG_SHIFT) | count);
-      // Issue both first windows now: in-group predecessors (newest first)
-      // and the groups before this one.
-      // Window loads are clamped to valid slots; slots outside the window
-      // are masked when the window is consumed, so the loads stay in flight
-      // until then.
-#pragma unroll
-      for (int w = 0; w < LOOKBACK; ++w)
-        lb[w] = load_agent(&lbuf.tile[size_t(max(static_cast<int>(tile) - 1 - w, 0)) * BINS + tid]);
-#pragma unroll
-      for (int w = 0; w < GWIN; ++w) {
-        const size_t g = size_t(max(static_cast<int>(group) - 1 - w, 0));
-        gi[w] = load_agent(&lbuf.ginc[g * BINS + tid]);
-        ga[w] = load_agent(&lbuf.gagg[g * BINS + tid]);
-      }
-      tile_inc = wave_inclusive_sum(count, lane);
-      if (lane == 63) wave_sum[wave] = tile_inc;
-    }
-    __syncthreads();
-    uint32_t tile_start = 0;
-    if (tid < BINS) {
-      tile_start = tile_inc - count;
-      for (uint32_t w = 0; w < wave; ++w) tile_start += wave_sum[w];
-#pragma unroll
-      for (int w = 0; w < SUBS; ++w) hist[w][tid] = static_cast<uint16_t>(hist[w][tid] + tile_start);
-    }
-    if (tid < SUBS) hist[tid][DUMMY] = TILE;  // dummy items stage into the spare slot
-#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT < 2
-    if (tid == CLAIM) s_tile = claimed;
-#endif
-    __syncthreads();
-#if !RCCL_RADIX_PERSISTENT
-    const uint32_t next = num_tiles;
-#elif RCCL_RADIX_CLAIM_POINT < 2
-    const uint32_t next = s_tile;
-#else
-    if (tid == CLAIM) claimed = add_agent(tile_counter, 1u);
-#endif
-
-    // Stage keys in digit order. The empty asm statements stop the compiler
-    // from keeping per-item digit addresses alive from the ranking loop
-    // (recomputing them is cheaper than the registers).
-    uint32_t slane = sl;
-    asm volatile("" : "+v"(slane));
-    const uint16_t *shist = hist[sw];
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) asm volatile("" : "+v"(key[j]));
-    // In batches: the batch's offset reads are in flight together before its
-    // staging writes.
-#pragma unroll
-    for (int j0 = 0; j0 < ITEMS; j0 += BATCH) {
-      uint32_t base[BATCH];
-#pragma unroll
-      for (int b = 0; b < BATCH && j0 + b < ITEMS; ++b) {
-        const int j = j0 + b;
-        const uint32_t d =
-            uint32_t(j) * 32 + slane < sub_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
-        base[b] = shist[d];
-      }
-#pragma unroll
-      for (int b = 0; b < BATCH && j0 + b < ITEMS; ++b) {
-        const int j = j0 + b;
-        rank[j] = min(rank[j] + base[b], uint32_t(TILE));
-        stage_keys[rank[j]] = key[j];
-      }
-    }
-
-    // Prefetch the next tile's keys into the key registers (the current keys
-    // live in LDS now); they land while this tile's look-back and scatter
-    // run. No branch around the loads: past the last tile every element is
-    // masked off, and a fixed count of loads lets the look-back wait for its
-    // own window loads only.
-#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT < 2
-    const size_t next_sub_base = size_t(next) * TILE + size_t(sw) * SUB_ITEMS;
+    key[j] = keys_in[min(wave_base + size_t(j) * 64 + lane, last_item)];
+  ValReg val[ITEMS];
+  if constexpr (PAIRS) {
+    // Issued now, consumed after the key scatter.
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j)
-      key[j] = keys_in[min(next_sub_base + size_t(j) * 32 + sl, last_item)];
-#endif
+      val[j] = vals_in[min(wave_base + size_t(j) * 64 + lane, last_item)];
+  }
+  const uint32_t wave_valid =
+      n > wave_base ? static_cast<uint32_t>(min<size_t>(n - wave_base, WAVE_ITEMS)) : 0u;
+  lds_barrier();
+  // Wait for all the keys (not the values) before counting: one wait here is
+  // measurably faster than the per-item waits the compiler would interleave
+  // with the counting atomics.
+  wait_vmcnt<PAIRS ? ITEMS : 0>();
 
-    // Two-level decoupled look-back, one thread per digit, consuming the
-    // windows issued above newest first. In-group predecessors are summed
-    // tile by tile until an inclusive prefix or the group start; earlier
-    // groups are then summed whole (complete aggregates) until a group's
-    // inclusive prefix. A slot that is not yet published is polled again.
-    if (tid < BINS) {
-      Desc excl = 0;
-      bool done = tile == 0;
-      // Window slot w holds tile t - w; slots before the group are boundaries.
-      int t = static_cast<int>(tile) - 1;
-      auto eat_tiles = [&]() {
-        int consumed = 0;
-        bool stop = false;
+  // Per-wave digit counts.
+  uint32_t *wcnt = cnt[wave];
 #pragma unroll
-        for (int w = 0; w < LOOKBACK; ++w) {
-          if (!done && !stop) {
-            const Desc v = t - w >= gfirst ? lb[w] : DI::BOUNDARY;
-            const Desc flag = v >> DI::SHIFT;
-            if (flag == 0 || flag == (DI::BOUNDARY >> DI::SHIFT)) {
-              stop = true;
-            } else {
-              excl += v & DI::MASK;
-              ++consumed;
-              done = flag == (DI::INCL >> DI::SHIFT);
-            }
-          }
-        }
-        t -= consumed;
-        return consumed;
-      };
-      // Group slot w holds group g - w; slots before group 0 read as an
-      // inclusive zero.
-      int g = static_cast<int>(group) - 1;
-      auto eat_groups = [&]() {
-        int consumed = 0;
-        bool blocked = false;
-#pragma unroll
-        for (int w = 0; w < GWIN; ++w) {
-          if (!done && !blocked) {
-            const bool real = g - w >= 0;
-            const Desc vi = real ? gi[w] : DI::INCL;
-            const uint32_t va = real ? ga[w] : 0u;
-            if ((vi >> DI::SHIFT) == (DI::INCL >> DI::SHIFT)) {
-              excl += vi & DI::MASK;
-              done = true;
-            } else if ((va >> GAGG_SHIFT) == uint32_t(GROUP)) {
-              excl += va & GAGG_MASK;  // earlier groups are always full
-              ++consumed;
-            } else {
-              blocked = true;
-            }
-          }
-        }
-        g -= consumed;
-        return consumed;
-      };
-      // The first windows were issued before the staging; they are consumed
-      // outside the polling loops so that waiting for them does not wait for
-      // the prefetch issued after them.
-      if (!done) {
-        int c = eat_tiles();
-        while (!done && t >= gfirst) {
-          if (c == 0) __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-          for (int w = 0; w < LOOKBACK; ++w)
-            lb[w] = load_agent(&lbuf.tile[size_t(max(t - w, 0)) * BINS + tid]);
-          c = eat_tiles();
-        }
-      }
-      if (!done) {
-        int c = eat_groups();
-        while (!done) {
-          if (c == 0) __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-          for (int w = 0; w < GWIN; ++w) {
-            const size_t gg = size_t(max(g - w, 0));
-            gi[w] = load_agent(&lbuf.ginc[gg * BINS + tid]);
-            ga[w] = load_agent(&lbuf.gagg[gg * BINS + tid]);
-          }
-          c = eat_groups();
-        }
-      }
-      const Desc incl = static_cast<Desc>(DI::INCL | (excl + Desc(count)));
-      if (tile > 0) store_agent(&lbuf.tile[size_t(tile) * BINS + tid], incl);
-      const uint32_t glast = min(uint32_t(gfirst + GROUP), num_tiles) - 1u;
-      if (tile == glast) store_agent(&lbuf.ginc[size_t(group) * BINS + tid], incl);
-      digit_off[tid] = bin_start + static_cast<uint32_t>(excl) - tile_start;
-    }
-#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT == 2
-    if (tid == CLAIM) s_tile = claimed;
-#endif
-    __syncthreads();
-#if RCCL_RADIX_PERSISTENT && RCCL_RADIX_CLAIM_POINT == 2
-    const uint32_t next = s_tile;
-    const size_t next_sub_base = size_t(next) * TILE + size_t(sw) * SUB_ITEMS;
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j)
-      key[j] = keys_in[min(next_sub_base + size_t(j) * 32 + sl, last_item)];
-#endif
+  for (int j = 0; j < ITEMS; ++j) {
+    const uint32_t d =
+        uint32_t(j) * 64 + lane < wave_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
+    __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  lds_barrier();
 
-    // Coalesced scatter: consecutive staged keys of one digit go to
-    // consecutive output positions.
-    const uint32_t valid_count = static_cast<uint32_t>(min<size_t>(TILE, n - tile_base));
-    // Positions are exact when the bins match the keys; the clamp only keeps
-    // a caller that changes the keys mid-sort from writing out of bounds.
-    const uint32_t last = static_cast<uint32_t>(n - 1);
-    // In batches: the batch's staged keys are read together, then their
-    // digits' offsets together, then stored; only the stores are predicated.
-    uint32_t dst[PAIRS ? ITEMS : 1];
+  // Per digit: the tile's count, published at once together with the first
+  // look-back windows (consumed after the ranking, so their latency hides
+  // behind it); then the block-wide exclusive scan over digits.
+  const uint32_t group = tile / GROUP;
+  const int gfirst = static_cast<int>(group) * GROUP;
+  uint32_t count = 0, tile_inc = 0;
+  uint32_t wc[WAVES];
+  Desc lb[LOOKBACK];
+  Desc gi[GWIN];
+  uint32_t ga[GWIN];
+  if (tid < BINS) {
 #pragma unroll
-    for (int k0 = 0; k0 < ITEMS; k0 += BATCH) {
-      Bits kk[BATCH];
-      uint32_t off[BATCH];
-#pragma unroll
-      for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b)
-        kk[b] = stage_keys[uint32_t(k0 + b) * THREADS + tid];
-#pragma unroll
-      for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b)
-        off[b] = digit_off[Ops::digit(kk[b], bit, mask)];
-#pragma unroll
-      for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b) {
-        const uint32_t i = uint32_t(k0 + b) * THREADS + tid;
-        const uint32_t p = min(off[b] + i, last);
-        if (i < valid_count) keys_out[p] = kk[b];
-        if constexpr (PAIRS) dst[k0 + b] = p;
-      }
+    for (int w = 0; w < WAVES; ++w) {
+      wc[w] = cnt[w][tid];
+      count += wc[w];
     }
-    if constexpr (PAIRS) {
-      __syncthreads();
-      Val *stage_vals = reinterpret_cast<Val *>(stage_raw);
+    store_agent(&lbuf.tile[size_t(tile) * BINS + tid],
+                static_cast<Desc>((tile == 0 ? DI::INCL : DI::AGG) | Desc(count)));
+    add_agent(&lbuf.gagg[size_t(group) * BINS + tid], (1u << GAGG_SHIFT) | count);
+    // Window loads are clamped to valid slots; slots outside the window are
+    // masked when the window is consumed.
 #pragma unroll
-      for (int j = 0; j < ITEMS; ++j) stage_vals[rank[j]] = val[j];
-      __syncthreads();
+    for (int w = 0; w < LOOKBACK; ++w)
+      lb[w] = load_agent(
+          &lbuf.tile[size_t(max(static_cast<int>(tile) - 1 - w, 0)) * BINS + tid]);
 #pragma unroll
-      for (int k = 0; k < ITEMS; ++k) {
-        const uint32_t i = uint32_t(k) * THREADS + tid;
-        if (i < valid_count) vals_out[dst[k]] = stage_vals[i];
-      }
+    for (int w = 0; w < GWIN; ++w) {
+      const size_t g = size_t(max(static_cast<int>(group) - 1 - w, 0));
+      gi[w] = load_agent(&lbuf.ginc[g * BINS + tid]);
+      ga[w] = load_agent(&lbuf.gagg[g * BINS + tid]);
     }
-    if (tid < BINS && lbuf_next.tile) {
-      lbuf_next.tile[size_t(tile) * BINS + tid] = 0;
-      if (static_cast<int>(tile) == gfirst) {
-        lbuf_next.ginc[size_t(group) * BINS + tid] = 0;
-        lbuf_next.gagg[size_t(group) * BINS + tid] = 0;
-      }
+    tile_inc = wave_inclusive_sum(count, lane);
+    if (lane == 63) wave_sum[wave] = tile_inc;
+  }
+  lds_barrier();
+  uint32_t tile_start = 0;
+  if (tid < BINS) {
+    tile_start = tile_inc - count;
+    for (uint32_t w = 0; w < wave; ++w) tile_start += wave_sum[w];
+    // Each wave's counter becomes the tile position of its first key of this
+    // digit.
+    uint32_t run = tile_start;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      cnt[w][tid] = run;
+      run += wc[w];
     }
-    __syncthreads();
+  }
+  if (tid < WAVES) cnt[tid][DUMMY] = TILE;
+  lds_barrier();
 
-    if (next >= num_tiles) break;
-#if RCCL_RADIX_PERSISTENT
-    tile = next;
-    sub_base = next_sub_base;
-#endif
+  // Rank and stage. The digits are recomputed: an opaque copy of the keys
+  // stops the compiler from keeping all of them (or their counter addresses)
+  // alive from the counting loop. The returning atomic hands equal digits
+  // consecutive positions in lane order, which with the item loop and the
+  // per-wave counters is source order; dummies all land in the spare slot.
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) asm volatile("" : "+v"(key[j]));
+  // All atomics are issued before the first staging write, so the round
+  // trips overlap; the opaque copy of the positions keeps the compiler from
+  // pairing each write with its atomic (which serialises them).
+  uint32_t pos[ITEMS];
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const uint32_t d =
+        uint32_t(j) * 64 + lane < wave_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
+    pos[j] = __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) asm volatile("" : "+v"(pos[j]));
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    pos[j] = min(pos[j], uint32_t(TILE));
+    stage_keys[pos[j]] = key[j];
+  }
+
+  if (tid < BINS) {
+    const Desc excl = lookback_consume<Desc>(lbuf, tile, group, tid, lb, gi, ga);
+    const Desc incl = static_cast<Desc>(DI::INCL | (excl + Desc(count)));
+    if (tile > 0) store_agent(&lbuf.tile[size_t(tile) * BINS + tid], incl);
+    const uint32_t glast = min(uint32_t(gfirst + GROUP), num_tiles) - 1u;
+    if (tile == glast) store_agent(&lbuf.ginc[size_t(group) * BINS + tid], incl);
+    digit_off[tid] = bin_start + static_cast<uint32_t>(excl) - tile_start;
+  }
+  lds_barrier();
+
+  // Coalesced scatter: consecutive staged keys of one digit go to consecutive
+  // output positions. Positions are exact when the bins match the keys; the
+  // clamp only keeps a caller that changes the keys mid-sort from writing out
+  // of bounds. In batches: the staged keys are read together, then their
+  // digits' offsets, then stored.
+  const size_t tile_base = size_t(tile) * TILE;
+  const uint32_t valid_count = static_cast<uint32_t>(min<size_t>(TILE, n - tile_base));
+  const uint32_t last = static_cast<uint32_t>(n - 1);
+  uint32_t dst[PAIRS ? ITEMS : 1];
+#pragma unroll
+  for (int k0 = 0; k0 < ITEMS; k0 += BATCH) {
+    Bits kk[BATCH];
+    uint32_t off[BATCH];
+#pragma unroll
+    for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b)
+      kk[b] = stage_keys[uint32_t(k0 + b) * THREADS + tid];
+#pragma unroll
+    for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b)
+      off[b] = digit_off[Ops::digit(kk[b], bit, mask)];
+#pragma unroll
+    for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b) {
+      const uint32_t i = uint32_t(k0 + b) * THREADS + tid;
+      const uint32_t p = min(off[b] + i, last);
+      if (i < valid_count) keys_out[p] = kk[b];
+      if constexpr (PAIRS) dst[k0 + b] = p;
+    }
+  }
+  if constexpr (PAIRS) {
+    lds_barrier();
+    Val *stage_vals = reinterpret_cast<Val *>(stage_raw);
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) stage_vals[pos[j]] = val[j];
+    lds_barrier();
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+      const uint32_t i = uint32_t(k) * THREADS + tid;
+      if (i < valid_count) vals_out[dst[k]] = stage_vals[i];
+    }
+  }
+  // Clear this tile's slots of the next pass's look-back buffer (it is not
+  // read before the next launch).
+  if (tid < BINS && lbuf_next.tile) {
+    lbuf_next.tile[size_t(tile) * BINS + tid] = 0;
+    if (static_cast<int>(tile) == gfirst) {
+      lbuf_next.ginc[size_t(group) * BINS + tid] = 0;
+      lbuf_next.gagg[size_t(group) * BINS + tid] = 0;
+    }
   }
 }
 
@@ -658,7 +602,7 @@ struct Layout {
   size_t tiles = 0;
   size_t groups = 0;
   size_t desc_bytes = 4;
-  size_t bins = 0, counters = 0;
+  size_t bins = 0;
   size_t lb[2] = {0, 0};  // look-back buffers: tile descriptors, group prefixes, aggregates
   size_t lb_ginc = 0, lb_gagg = 0, lb_bytes = 0;  // offsets/size within one buffer
   size_t total = 0;
@@ -682,7 +626,6 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
   constexpr int ITEMS = items_for(sizeof(Bits), VBYTES);
   constexpr int THREADS = threads_for(VBYTES);
   uint32_t *bins = reinterpret_cast<uint32_t *>(a.ws + l.bins);
-  uint32_t *counters = reinterpret_cast<uint32_t *>(a.ws + l.counters);
   LookbackBuf<Desc> lb[2];
   for (int b = 0; b < 2; ++b) {
     unsigned char *base = a.ws + l.lb[b];
@@ -693,7 +636,7 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
 
   {
     KernelTimer t("radix_init", a.stream, 0);
-    init_kernel<<<1, 256, 0, a.stream>>>(bins, counters, passes);
+    init_kernel<<<1, 256, 0, a.stream>>>(bins, passes);
   }
   RCCL_HIP_TRY(check_launch("radix init"));
 
@@ -714,8 +657,8 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
   }
   RCCL_HIP_TRY(check_launch("radix bins scan"));
 
-  // Persistent grid: as many blocks as fit on the device at once, but never
-  // more than there are tiles.
+  // The XCD-aware tile order needs the blocks of one row of runs (and the
+  // next) resident at once; every MI355X configuration holds far more.
   static int blocks_per_cu = 0;
   static int cus = 0;
   if (blocks_per_cu == 0) {
@@ -727,12 +670,10 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
       err = hipOccupancyMaxActiveBlocksPerMultiprocessor(
           &blocks_per_cu, onesweep_kernel<Bits, Val, Ops, ITEMS, Desc, THREADS>, THREADS, 0);
     if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "radix occupancy", err);
-    if (blocks_per_cu < 1 || cus < 1)
-      return set_error(RCCL_HIP_ERROR_LAUNCH, "radix onesweep does not fit on the device");
   }
-  const uint32_t grid = static_cast<uint32_t>(
-      RCCL_RADIX_PERSISTENT ? std::min<size_t>(l.tiles, size_t(blocks_per_cu) * size_t(cus))
-                            : l.tiles);
+  if (size_t(blocks_per_cu) * size_t(cus) < 2 * size_t(XCDS) * XCD_RUN)
+    return set_error(RCCL_HIP_ERROR_LAUNCH, "radix onesweep does not fit on the device");
+  const uint32_t grid = static_cast<uint32_t>(onesweep_grid(l.tiles));
 
   for (uint32_t p = 0; p < passes; ++p) {
     const uint32_t bit = a.begin_bit + 8u * p;
@@ -744,8 +685,8 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
         static_cast<const Bits *>(a.keys[in]), static_cast<Bits *>(a.keys[out]),
         static_cast<const Val *>(a.vals[in]), static_cast<Val *>(a.vals[out]), a.n,
         static_cast<uint32_t>(l.tiles), bins + size_t(p) * BINS, lb[p & 1],
-        p + 1 < passes ? lb[(p + 1) & 1] : LookbackBuf<Desc>{nullptr, nullptr, nullptr},
-        counters + p, bit, mask);
+        p + 1 < passes ? lb[(p + 1) & 1] : LookbackBuf<Desc>{nullptr, nullptr, nullptr}, bit,
+        mask);
     RCCL_HIP_TRY(check_launch("radix onesweep"));
     a.cur = out;
   }
@@ -777,6 +718,11 @@ rccl_hip_status run_values(SortArgs &a, size_t value_bytes, const Layout &l, uin
   }
   return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix value bytes");
 }
+
+// Runs lane_order_check_kernel once on the current device (see the onesweep
+// notes); RCCL_HIP_ERROR_UNSUPPORTED_TARGET if the LDS does not serve lanes of
+// one atomic in lane order.
+rccl_hip_status check_lane_order();
 
 // One entry per key kind, each compiled in its own translation unit.
 #define RCCL_RADIX_DECLARE_KIND(NAME)                                                   \
