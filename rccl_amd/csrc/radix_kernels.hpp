@@ -219,6 +219,91 @@ histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__
   }
 }
 
+// histogram32: the same for 4-byte keys, with per-lane counter columns. Lane
+// l of every wave counts into column l % HIST_COLS of its digit's row, so the
+// lanes of one LDS atomic hit at most two banks' worth of conflicts instead of
+// random ones (random digits into one shared row per wave cost about twice as
+// many LDS cycles per atomic). All four passes' rows take 64 KB: two blocks
+// per CU, grid-striding over chunks.
+#ifndef RCCL_RADIX_HIST32_THREADS
+#define RCCL_RADIX_HIST32_THREADS 512
+#endif
+#ifndef RCCL_RADIX_HIST32_ITEMS
+#define RCCL_RADIX_HIST32_ITEMS 16
+#endif
+#ifndef RCCL_RADIX_HIST_COLS
+#define RCCL_RADIX_HIST_COLS 16
+#endif
+constexpr int HIST32_THREADS = RCCL_RADIX_HIST32_THREADS;
+constexpr int HIST32_ITEMS = RCCL_RADIX_HIST32_ITEMS;
+constexpr int HIST_COLS = RCCL_RADIX_HIST_COLS;
+
+template <class Bits, class Ops>
+__global__ void __launch_bounds__(HIST32_THREADS)
+histogram32_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__ bins,
+                   uint32_t begin_bit, uint32_t end_bit, uint32_t passes,
+                   uint32_t *__restrict__ zero_words, size_t zero_count) {
+  static_assert(sizeof(Bits) == 4, "4-byte keys: at most four 8-bit passes");
+  constexpr int PMAX = 4;
+  __shared__ uint32_t hist[PMAX * BINS * HIST_COLS];  // [pass][digit][column]
+  const uint32_t tid = threadIdx.x;
+  for (uint32_t i = tid; i < passes * BINS * HIST_COLS; i += HIST32_THREADS) hist[i] = 0;
+  for (size_t i = size_t(blockIdx.x) * HIST32_THREADS + tid; i < zero_count;
+       i += size_t(gridDim.x) * HIST32_THREADS)
+    zero_words[i] = 0;
+  __syncthreads();
+
+  const uint32_t col = tid % HIST_COLS;
+  uint32_t shift[PMAX], dmask[PMAX];
+#pragma unroll
+  for (int p = 0; p < PMAX; ++p) {
+    const uint32_t bit = begin_bit + 8u * p;
+    shift[p] = bit;
+    dmask[p] = uint32_t(p) < passes ? (1u << min(8u, end_bit - bit)) - 1u : 0u;
+  }
+  // The next chunk's keys are loaded before the current chunk is counted, so
+  // the load latency hides behind the counting.
+  constexpr size_t CHUNK = size_t(HIST32_THREADS) * HIST32_ITEMS;
+  const size_t stride = size_t(gridDim.x) * CHUNK;
+  Bits next[HIST32_ITEMS];
+  auto load_chunk = [&](size_t base) {
+    const uint32_t avail = static_cast<uint32_t>(min<size_t>(n - base, CHUNK));
+#pragma unroll
+    for (int j = 0; j < HIST32_ITEMS; ++j)
+      next[j] = keys[base + min(uint32_t(j) * HIST32_THREADS + tid, avail - 1u)];
+  };
+  if (size_t(blockIdx.x) * CHUNK < n) load_chunk(size_t(blockIdx.x) * CHUNK);
+  for (size_t base = size_t(blockIdx.x) * CHUNK; base < n; base += stride) {
+    const uint32_t avail = static_cast<uint32_t>(min<size_t>(n - base, CHUNK));
+    Bits k[HIST32_ITEMS];
+#pragma unroll
+    for (int j = 0; j < HIST32_ITEMS; ++j) k[j] = next[j];
+    if (base + stride < n) load_chunk(base + stride);
+#pragma unroll
+    for (int j = 0; j < HIST32_ITEMS; ++j) {
+      if (uint32_t(j) * HIST32_THREADS + tid >= avail) continue;
+      const Bits s = Ops::digit_source(k[j]);
+#pragma unroll
+      for (int p = 0; p < PMAX; ++p) {
+        if (uint32_t(p) >= passes) break;
+        const uint32_t d = static_cast<uint32_t>(s >> shift[p]) & dmask[p];
+        __hip_atomic_fetch_add(&hist[(uint32_t(p) * BINS + d) * HIST_COLS + col], 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+  }
+  __syncthreads();
+  // Row sums. Thread e reads its row's columns in rotated order, so the
+  // threads of a wave read distinct banks.
+  for (uint32_t e = tid; e < passes * BINS; e += HIST32_THREADS) {
+    const uint32_t *row = &hist[e * HIST_COLS];
+    uint32_t sum = 0;
+#pragma unroll
+    for (uint32_t c = 0; c < HIST_COLS; ++c) sum += row[(c + e) % HIST_COLS];
+    if (sum) add_agent(&bins[e], sum);
+  }
+}
+
 // Turn every pass's digit counts into exclusive offsets (the first output
 // position of each digit), once, so the onesweep blocks read them instead of
 // each scanning the bins. One block of BINS threads. (Internal linkage, like
@@ -640,15 +725,34 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
   }
   RCCL_HIP_TRY(check_launch("radix init"));
 
-  const size_t chunk = size_t(HIST_THREADS) * HIST_ITEMS;
-  const size_t hist_blocks = std::max<size_t>(1, std::min<size_t>((a.n + chunk - 1) / chunk, 2048));
   const size_t zero_words = l.lb_bytes / sizeof(uint32_t);
+  static int hist_cus = 0;
+  if (hist_cus == 0) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err == hipSuccess)
+      err = hipDeviceGetAttribute(&hist_cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "radix device", err);
+  }
   {
     KernelTimer t("radix_histogram", a.stream, a.n);
-    histogram_kernel<Bits, Ops><<<dim3(static_cast<uint32_t>(hist_blocks)), HIST_THREADS, 0,
-                                  a.stream>>>(
-        static_cast<const Bits *>(a.keys[a.cur]), a.n, bins, a.begin_bit, a.end_bit, passes,
-        reinterpret_cast<uint32_t *>(a.ws + l.lb[0]), zero_words);
+    if constexpr (sizeof(Bits) == 4) {
+      const size_t chunk = size_t(HIST32_THREADS) * HIST32_ITEMS;
+      const size_t per_cu = (160 * 1024) / (4 * BINS * HIST_COLS * sizeof(uint32_t));
+      const size_t blocks = std::max<size_t>(
+          1, std::min<size_t>((a.n + chunk - 1) / chunk, size_t(hist_cus) * per_cu));
+      histogram32_kernel<Bits, Ops><<<dim3(static_cast<uint32_t>(blocks)), HIST32_THREADS, 0,
+                                      a.stream>>>(
+          static_cast<const Bits *>(a.keys[a.cur]), a.n, bins, a.begin_bit, a.end_bit, passes,
+          reinterpret_cast<uint32_t *>(a.ws + l.lb[0]), zero_words);
+    } else {
+      const size_t chunk = size_t(HIST_THREADS) * HIST_ITEMS;
+      const size_t blocks = std::max<size_t>(1, std::min<size_t>((a.n + chunk - 1) / chunk, 2048));
+      histogram_kernel<Bits, Ops><<<dim3(static_cast<uint32_t>(blocks)), HIST_THREADS, 0,
+                                    a.stream>>>(
+          static_cast<const Bits *>(a.keys[a.cur]), a.n, bins, a.begin_bit, a.end_bit, passes,
+          reinterpret_cast<uint32_t *>(a.ws + l.lb[0]), zero_words);
+    }
   }
   RCCL_HIP_TRY(check_launch("radix histogram"));
   {
