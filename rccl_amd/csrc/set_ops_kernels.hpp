@@ -24,7 +24,7 @@ namespace set_ops {
 
 using ordering::NoValue;
 
-constexpr int THREADS = 256;
+constexpr int THREADS = 512;
 constexpr int WAVES = THREADS / 64;
 constexpr int GROUP = 64;  // tiles per look-back group (one wave polls a group)
 
@@ -57,7 +57,12 @@ __device__ __forceinline__ void balanced_path(RA a, size_t na, RB b, size_t nb, 
   size_t i = ordering::merge_path<K>(a, na, b, nb, diag, less);
   const size_t j = diag - i;
   size_t star = 0;
-  if (j < nb) {
+  // No A item before the split and no B item before it is equal to B[j]:
+  // the balanced path is the merge path (the searches below would find
+  // i_start = i, j_start = j and move nothing).
+  const bool run_straddles =
+      j < nb && ((i > 0 && !less(a(i - 1), b(j))) || (j > 0 && !less(b(j - 1), b(j))));
+  if (run_straddles) {
     const K key = b(j);
     size_t lo = 0, hi = i;  // first A in [0, i) not before key
     while (lo < hi) {
@@ -133,6 +138,7 @@ struct TileSmem {
   uint32_t split_b[THREADS + 1];
   uint32_t wave_total[WAVES];
   uint64_t tile_offset;
+  uint32_t tile;
 };
 
 // One serial step of operation OP on the current heads. Mirrors the four
@@ -180,7 +186,8 @@ __global__ void __launch_bounds__(THREADS)
 tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restrict__ b,
             const V *__restrict__ bv, const uint64_t *__restrict__ splits, size_t tiles,
             K *__restrict__ out, V *__restrict__ outv, size_t out_cap,
-            uint64_t *__restrict__ out_count, uint64_t *desc, uint64_t *gagg, uint64_t *ginc) {
+            uint64_t *__restrict__ out_count, uint64_t *desc, uint64_t *gagg, uint64_t *ginc,
+            uint32_t *ticket) {
   using Smem = TileSmem<K, V, ITEMS>;
   constexpr bool PAIRS = Smem::PAIRS;
   constexpr bool VALS_B = PAIRS && (OP == UNION || OP == SYMMETRIC_DIFFERENCE);
@@ -189,19 +196,42 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
-  const size_t t = blockIdx.x;
+  // Tiles are numbered in the order blocks start (an atomic ticket), so every
+  // tile a look-back waits on has started earlier; block indices would not
+  // guarantee that, since the XCDs dispatch their blocks at their own pace.
+  if (tid == 0) sm.tile = add_agent(ticket, 1u);
+  __syncthreads();
+  const size_t t = sm.tile;
   const size_t i0 = splits[2 * t], j0 = splits[2 * t + 1];
   const size_t i1 = splits[2 * t + 2], j1 = splits[2 * t + 3];
   const uint32_t la = static_cast<uint32_t>(i1 - i0);
   const uint32_t lb = static_cast<uint32_t>(j1 - j0);
   const uint32_t len = la + lb;
 
-  // Stage A then B (striped, coalesced).
-  for (uint32_t i = tid; i < len; i += THREADS) {
-    sm.keys[i] = i < la ? a[i0 + i] : b[j0 + (i - la)];
-    if constexpr (PAIRS) {
-      if (i < la) sm.vals[i] = av[i0 + i];
-      else if constexpr (VALS_B) sm.vals[i] = bv[j0 + (i - la)];
+  // Stage A then B (striped, coalesced). A fixed, unrolled number of loads
+  // per thread, all issued before the first LDS write; each item loads from
+  // A or B through a per-lane address, clamped to the tile's last item.
+  {
+    constexpr int STAGE = (Smem::CAP + THREADS - 1) / THREADS;
+    K kr[STAGE];
+    typename std::conditional<PAIRS, V, char>::type vr[PAIRS ? STAGE : 1];
+#pragma unroll
+    for (int k = 0; k < STAGE; ++k) {
+      const uint32_t i = min(uint32_t(k) * THREADS + tid, len ? len - 1u : 0u);
+      const bool from_a = i < la;
+      kr[k] = len ? *(from_a ? a + i0 + i : b + j0 + (i - la)) : K{};
+      if constexpr (PAIRS) {
+        if constexpr (VALS_B) vr[k] = len ? *(from_a ? av + i0 + i : bv + j0 + (i - la)) : V{};
+        else vr[k] = from_a ? av[i0 + i] : V{};
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < STAGE; ++k) {
+      const uint32_t i = uint32_t(k) * THREADS + tid;
+      if (i < len) {
+        sm.keys[i] = kr[k];
+        if constexpr (PAIRS) sm.vals[i] = vr[k];
+      }
     }
   }
   __syncthreads();
@@ -231,11 +261,13 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
   K outk[ITEMS];
   uint32_t src[PAIRS ? ITEMS : 1];
   uint32_t mask = 0;
+  // The heads live in registers; a step reloads only the side it advanced.
+  const uint32_t last = len ? len - 1u : 0u;
+  K ka = sm.keys[min(ia, last)];
+  K kb = sm.keys[min(la + ib, last)];
 #pragma unroll
   for (int k = 0; k < ITEMS; ++k) {
     const bool a_ok = ia < ea, b_ok = ib < eb;
-    const K ka = sm.keys[min(ia, len ? len - 1 : 0u)];
-    const K kb = sm.keys[min(la + ib, len ? len - 1 : 0u)];
     bool emit, emit_b, adv_a, adv_b;
     serial_step<OP, K>(ka, kb, a_ok, b_ok, less, emit, emit_b, adv_a, adv_b);
     outk[k] = emit_b ? kb : ka;
@@ -243,6 +275,10 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
     mask |= emit ? (1u << k) : 0u;
     ia += adv_a ? 1u : 0u;
     ib += adv_b ? 1u : 0u;
+    if (k + 1 < ITEMS) {
+      if (adv_a) ka = sm.keys[min(ia, last)];
+      if (adv_b) kb = sm.keys[min(la + ib, last)];
+    }
   }
   const uint32_t mine = __popc(mask);
   V outv_reg[PAIRS ? ITEMS : 1];
@@ -348,9 +384,14 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
     }
   }
   __syncthreads();
-  for (uint32_t i = tid; i < keep; i += THREADS) {
-    out[base + i] = sm.keys[i];
-    if constexpr (PAIRS) outv[base + i] = sm.vals[i];
+  constexpr int STORE = (Smem::CAP + THREADS - 1) / THREADS;
+#pragma unroll
+  for (int k = 0; k < STORE; ++k) {
+    const uint32_t i = uint32_t(k) * THREADS + tid;
+    if (i < keep) {
+      out[base + i] = sm.keys[i];
+      if constexpr (PAIRS) outv[base + i] = sm.vals[i];
+    }
   }
 }
 
@@ -371,7 +412,7 @@ struct SetArgs {
 
 struct Layout {
   size_t tiles = 0, groups = 0;
-  size_t splits = 0, desc = 0, gagg = 0, ginc = 0, total = 0;
+  size_t splits = 0, desc = 0, gagg = 0, ginc = 0, ticket = 0, total = 0;
 };
 
 template <class K, class V>
@@ -390,6 +431,8 @@ Layout layout(size_t na, size_t nb) {
   off += l.groups * sizeof(uint64_t);
   l.ginc = off;
   off += l.groups * sizeof(uint64_t);
+  l.ticket = off;
+  off += sizeof(uint64_t);
   l.total = align_up(off, 256);
   return l;
 }
@@ -407,7 +450,9 @@ rccl_hip_status run_op(const SetArgs &s) {
   uint64_t *desc = reinterpret_cast<uint64_t *>(ws + l.desc);
   uint64_t *gagg = reinterpret_cast<uint64_t *>(ws + l.gagg);
   uint64_t *ginc = reinterpret_cast<uint64_t *>(ws + l.ginc);
-  const size_t state_words = l.tiles + 2 * l.groups;
+  uint32_t *ticket = reinterpret_cast<uint32_t *>(ws + l.ticket);
+  // Descriptors, group words and the ticket are contiguous.
+  const size_t state_words = l.tiles + 2 * l.groups + 1;
   {
     KernelTimer t("set_clear", s.stream, state_words);
     clear_kernel<<<dim3(static_cast<uint32_t>(std::min<size_t>((state_words + 255) / 256, 1024))),
@@ -428,7 +473,7 @@ rccl_hip_status run_op(const SetArgs &s) {
                                         s.stream>>>(
         static_cast<const K *>(s.a), static_cast<const V *>(s.av), static_cast<const K *>(s.b),
         static_cast<const V *>(s.bv), splits, l.tiles, static_cast<K *>(s.out),
-        static_cast<V *>(s.outv), s.out_cap, s.out_count, desc, gagg, ginc);
+        static_cast<V *>(s.outv), s.out_cap, s.out_count, desc, gagg, ginc, ticket);
   }
   return check_launch("set tile");
 }
