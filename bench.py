@@ -114,7 +114,8 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_2p28.txt")
 def profiled_traffic(kernel, log2n):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
     summary (FETCH_SIZE and WRITE_SIZE scaled by a copy kernel of known size),
-    or None when that summary does not cover this problem size."""
+    or None when that summary does not cover this problem size (the summary
+    is of the default run, whose sizes all derive from --log2n 28)."""
     if log2n != 28 or not os.path.exists(TRAFFIC_PROFILE):
         return None
     with open(TRAFFIC_PROFILE) as f:
@@ -223,7 +224,8 @@ def run_merge(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup):
         "value": round(total / (ms * 1e-3) / 1e9, 3), "unit": "Gkeys/s (outputs)",
         "ms_per_step": round(ms, 4), "ms_per_step_wall": round(wall, 4),
         "bytes_model": "16 B/output = 8 B read (key + value) + 8 B written",
-        "roofline": roofline(16.0 * total, kms["merge"], "merge (one launch merges everything)"),
+        "roofline": roofline(16.0 * total, kms["merge"], "merge (one launch merges everything)",
+                             profiled_traffic("merge", log2_each + 1)),
         "kernel_ms": _rounded(kms), "validated": bool(ok),
     }
     del a, pa, b, pb, A, PA, B, PB, out, outv, ws
@@ -254,7 +256,8 @@ def run_merge_sort(torch, np, cub, abi, DeviceBuffer, wd, log2n, steps, warmup):
         "merge_passes": passes,
         "bytes_model": f"{8 * (1 + passes)} B/key = 8 B (block sort) + 8 B per merge pass",
         "roofline": roofline(8.0 * n, kms["merge_sort_pass"],
-                             "merge_sort_pass (one pass: 4n read + 4n write)"),
+                             "merge_sort_pass (one pass: 4n read + 4n write)",
+                             profiled_traffic("merge_sort_pass", log2n + 2)),
         "sort_roofline_frac": round(8.0 * (1 + passes) * n / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "kernel_ms": _rounded(kms), "validated": bool(ok),
     }
@@ -291,7 +294,8 @@ def run_set_ops(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup)
             "ms_per_step": round(ms, 4), "output": m,
             "value": round(2 * n_each / (ms * 1e-3) / 1e9, 3), "unit": "Gkeys/s (inputs)",
             "roofline": roofline(16.0 * n_each + 8.0 * m, kms["set_tile"],
-                                 "set_tile (reads both inputs, writes the result)"),
+                                 "set_tile (reads both inputs, writes the result)",
+                                 profiled_traffic("set_tile_" + op, log2_each + 2)),
             "kernel_ms": _rounded(kms), "validated": bool(ok),
         }
     del a, b, A, B, out
