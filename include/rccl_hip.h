@@ -111,7 +111,10 @@ RCCL_HIP_API int rccl_hip_abi_version(void);
 /* Check that `device` is a gfx950 GPU the kernels were built for. Replaces
  * Program::load (rccl-cub/src/cuda.rs:749-756, rccl-thrust/src/cuda.rs:85-91)
  * and the target gate ensure_radix_target (rccl-cub/src/radix.rs:14-22).
- * Returns UNSUPPORTED_TARGET on any other architecture. */
+ * Returns UNSUPPORTED_TARGET on any other architecture. On first use of a
+ * device it also runs a one-block check that the LDS serves the lanes of one
+ * atomic hitting the same address in lane order (the radix ranking relies on
+ * it) and returns UNSUPPORTED_TARGET if it does not. */
 RCCL_HIP_API rccl_hip_status rccl_hip_program_load(int device);
 
 /* ------------------------------------------------------------------------
