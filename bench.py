@@ -168,28 +168,50 @@ def run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, values_t, steps, warmup
             "launches": launches, "validated": bool(ok)}
 
 
-def cpu_baseline(keys_h, seconds, log2_sample):
-    """Oracle LSD radix sort (single thread) on the first 2^log2_sample keys
-    of the same input, repeated for about `seconds`."""
-    import oracle
-
-    n = keys_h.size
-    k = keys_h.copy()
+def _rate(fn, keys, seconds):
+    """Gkeys/s of fn(keys) repeated for about `seconds` (at least once)."""
     reps = 0
     t0 = time.perf_counter()
     while True:
-        oracle.radix_sort("u32", k)
+        fn(keys)
         reps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
-            break
+            return reps * keys.size / el / 1e9, reps, el
+
+
+def cpu_baseline(keys_h, seconds, log2_sample):
+    """Host sorts of the first 2^log2_sample keys of the metric input, timed on
+    this machine's cores: the headline is a parallel comparison sort on every
+    core this process may use (at most 16, the GPU box's CPU share), the
+    substitute for the reference's rayon par_sort; beside it a single-thread
+    std::sort (slice::sort_unstable substitute) and the oracle's LSD radix
+    sort on 2^24 keys."""
+    import oracle
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    par, par_reps, par_el = _rate(lambda k: oracle.par_sort_unstable_u32(k, threads), keys_h,
+                                  seconds * 0.5)
+    small = keys_h[: 1 << min(24, log2_sample)]
+    one, one_reps, one_el = _rate(oracle.sort_unstable_u32, small, seconds * 0.3)
+    lsd, lsd_reps, lsd_el = _rate(lambda k: oracle.radix_sort("u32", k), small, seconds * 0.2)
     return {
-        "value": round(reps * n / el / 1e9, 4),
+        "value": round(par, 4),
         "unit": "Gkeys/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"oracle/oracle.c stable LSD radix sort (8-bit passes) over the first "
-                  f"2^{log2_sample} keys of the benchmark input, {reps} sorts in {el:.1f} s",
+        "sample": f"oracle/oracle_sort.cpp parallel sort (per-thread std::sort + merge-path "
+                  f"merges; substitute for rayon par_sort, no Rust toolchain here) over the "
+                  f"first 2^{log2_sample} keys of the benchmark input on {threads} threads, "
+                  f"{par_reps} sorts in {par_el:.1f} s",
+        "single_thread": {
+            "value": round(one, 4), "unit": "Gkeys/s", "cores": 1,
+            "sample": f"std::sort (slice::sort_unstable substitute) over the first "
+                      f"2^{small.size.bit_length() - 1} keys, {one_reps} sorts in {one_el:.1f} s"},
+        "lsd_radix_1core": {
+            "value": round(lsd, 4), "unit": "Gkeys/s", "cores": 1,
+            "sample": f"oracle/oracle.c stable LSD radix sort (8-bit passes) over the first "
+                      f"2^{small.size.bit_length() - 1} keys, {lsd_reps} sorts in {lsd_el:.1f} s"},
     }
 
 
@@ -417,7 +439,7 @@ def main():
                                            "symmetric_difference"))
     if not args.no_cpu_baseline:
         _log("cpu baseline")
-        log_sample = min(24, args.log2n)
+        log_sample = min(26, args.log2n)
         out["cpu_baseline"] = cpu_baseline(workloads.metric_u32_keys(1 << log_sample),
                                            args.cpu_seconds, log_sample)
     out["validated"] = bool(valid)

@@ -67,6 +67,10 @@ def _load():
         lib.oracle_set_op.argtypes = [c.c_int, c.c_int, c.c_int, c.c_void_p, c.c_void_p,
                                       c.c_size_t, c.c_void_p, c.c_void_p, c.c_size_t,
                                       c.c_void_p, c.c_void_p, c.c_size_t]
+        lib.oracle_sort_unstable_u32.restype = c.c_int
+        lib.oracle_sort_unstable_u32.argtypes = [c.c_void_p, c.c_size_t]
+        lib.oracle_par_sort_unstable_u32.restype = c.c_int
+        lib.oracle_par_sort_unstable_u32.argtypes = [c.c_void_p, c.c_size_t, c.c_int]
         _lib = lib
     return _lib
 
@@ -156,3 +160,21 @@ def set_op(op, kind, a_keys, b_keys, a_values=None, b_values=None, descending=Fa
         raise ValueError("invalid set operation arguments")
     out = out[:n]
     return (out, out_v[:n]) if out_v is not None else out
+
+
+def sort_unstable_u32(keys):
+    """std::sort of a copy of u32 `keys` (the slice::sort_unstable substitute
+    of the CPU baseline; oracle_sort.cpp)."""
+    k = np.ascontiguousarray(keys, dtype=np.uint32).copy()
+    if _load().oracle_sort_unstable_u32(_ptr(k), k.size) != 0:
+        raise ValueError("oracle_sort_unstable_u32 failed")
+    return k
+
+
+def par_sort_unstable_u32(keys, threads):
+    """Parallel sort of a copy of u32 `keys` on `threads` threads (the
+    parallel-sort substitute of the CPU baseline; oracle_sort.cpp)."""
+    k = np.ascontiguousarray(keys, dtype=np.uint32).copy()
+    if _load().oracle_par_sort_unstable_u32(_ptr(k), k.size, int(threads)) != 0:
+        raise ValueError("oracle_par_sort_unstable_u32 failed")
+    return k

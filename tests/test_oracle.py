@@ -300,3 +300,17 @@ def test_splitmix64_known_answer():
     # splitmix64 finaliser of state 0 (Steele, Lea and Flood 2014; the
     # constants of Java's SplittableRandom).
     assert oracle.splitmix64(0) == 0xE220A8397B1DCDAF
+
+
+@pytest.mark.parametrize("n", [0, 1, 7, 1000, 65537, 1 << 20])
+@pytest.mark.parametrize("threads", [1, 3, 8, 16])
+def test_cpu_baseline_sorts_vs_numpy(n, threads):
+    """The CPU baseline's comparison sorts (std::sort and the threaded
+    chunk-sort + merge-path merges) against numpy's sort, with heavy
+    duplicates so ties cross chunk and slice boundaries."""
+    rng = np.random.default_rng(n * 31 + threads)
+    keys = rng.integers(0, max(1, n // 8) + 1, size=n, dtype=np.uint64).astype(np.uint32)
+    keys[: n // 3] = rng.integers(0, 1 << 32, size=n // 3, dtype=np.uint64).astype(np.uint32)
+    want = np.sort(keys)
+    assert np.array_equal(oracle.sort_unstable_u32(keys), want)
+    assert np.array_equal(oracle.par_sort_unstable_u32(keys, threads), want)
