@@ -4,7 +4,8 @@
 Metric: Gkeys/s radix sort at 2^28 for u32 keys (the headline
 ``value``) and for u64-key/u32-value pairs (reported under ``pairs``), with the
 fraction of the 8 TB/s HBM roofline. The C4 merge / merge sort and C5 set
-operation shapes are reported under ``ordering``.
+operation shapes, and the reference's record-sort benchmark, are reported
+under ``ordering``.
 
 A step is one full pass of the operation over the resident input. Radix sort
 is in place, so before every step its input is restored from a pristine
@@ -59,8 +60,11 @@ def _buffer(torch, DeviceBuffer, t, np_dtype):
 
 
 def time_steps(torch, abi, stream, steps, warmup, step, before=None):
-    """Run `step` warmup + steps times; returns (mean event ms, min, wall ms,
-    {kernel: mean ms}, {kernel: launches per step})."""
+    """Run `step` warmup times, then `steps` timed times, then `steps` more
+    with the library's per-launch timing on. Returns (mean event ms, min, wall
+    ms, {kernel: mean ms}, {kernel: launches per step}, [[(kernel, ms), ...]
+    per profiled step]). The timed steps run without per-launch events, so
+    ``ms_per_step`` carries no timing overhead."""
     for _ in range(warmup):
         if before:
             before()
@@ -68,9 +72,6 @@ def time_steps(torch, abi, stream, steps, warmup, step, before=None):
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    abi.timing_read()
-    abi.timing_enable(True)
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(steps):
         if before:
@@ -80,15 +81,24 @@ def time_steps(torch, abi, stream, steps, warmup, step, before=None):
         ends[k].record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    abi.timing_enable(False)
-    records = abi.timing_read()
     step_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    abi.timing_read()
+    abi.timing_enable(True)
+    per_step = []
+    for _ in range(steps):
+        if before:
+            before()
+        step()
+        torch.cuda.synchronize()
+        per_step.append([(name, kms) for name, kms, _items in abi.timing_read()])
+    abi.timing_enable(False)
     per = {}
-    for name, kms, _items in records:
-        per.setdefault(name, []).append(kms)
+    for launches in per_step:
+        for name, kms in launches:
+            per.setdefault(name, []).append(kms)
     return (sum(step_ms) / steps, min(step_ms), (t1 - t0) * 1e3 / steps,
             {k: sum(v) / len(v) for k, v in per.items()},
-            {k: len(v) // steps for k, v in per.items()})
+            {k: len(v) // steps for k, v in per.items()}, per_step)
 
 
 def roofline(bytes_per_launch, launch_ms, kernel, traffic=None):
@@ -157,7 +167,7 @@ def run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, values_t, steps, warmup
         else:
             cub.device_radix_sort_keys(launch, keys, ws)
 
-    ms, ms_min, wall, kms, launches = time_steps(torch, abi, launch.stream(), steps, warmup,
+    ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, launch.stream(), steps, warmup,
                                                  sort, restore)
     bits = 32 if kdt == np.uint32 else 64
     ok = _nondecreasing(torch, keys.tensor, bits)
@@ -230,7 +240,7 @@ def run_merge(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup):
     def step():
         cub.device_merge_pairs(launch, A, PA, B, PB, ws, out, outv)
 
-    ms, ms_min, wall, kms, launches = time_steps(torch, abi, launch.stream(), steps, warmup, step)
+    ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, launch.stream(), steps, warmup, step)
     total = 2 * n_each
     ok = _nondecreasing(torch, out.tensor, 32)
     ok = ok and _fingerprint(torch, out.tensor) == tuple(
@@ -266,7 +276,7 @@ def run_merge_sort(torch, np, cub, abi, DeviceBuffer, wd, log2n, steps, warmup):
     def step():
         cub.device_merge_sort_keys_copy(launch, src, ws, out)
 
-    ms, ms_min, wall, kms, launches = time_steps(torch, abi, launch.stream(), steps, warmup, step)
+    ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, launch.stream(), steps, warmup, step)
     ok = _nondecreasing(torch, out.tensor, 32)
     ok = ok and _fingerprint(torch, out.tensor) == _fingerprint(torch, keys_t)
     passes = launches.get("merge_sort_pass", 0)
@@ -309,7 +319,7 @@ def run_set_ops(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup)
         def step(op=op, ws=ws):
             cub.device_set_keys(launch, op, A, B, ws, out)
 
-        ms, ms_min, wall, kms, _ = time_steps(torch, abi, launch.stream(), steps, warmup, step)
+        ms, ms_min, wall, kms, _, _ = time_steps(torch, abi, launch.stream(), steps, warmup, step)
         m = ws.count()
         ok = m == want[op] and _nondecreasing(torch, out.tensor[:m], 64)
         results[op] = {
@@ -328,6 +338,74 @@ def run_set_ops(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup)
         "bytes_model": "8 B read per input key + 8 B written per output key",
         **results,
     }
+
+
+def run_record_sort(torch, np, abi, DeviceBuffer, wd, workloads, steps, warmup):
+    """The reference's record-sort benchmark (rccl-thrust/examples/
+    record_sort_benchmark.rs, benchmarks/cub-record-sort-reference.cu):
+    2^20 + 13 rows of [u32; 4] with u64 payloads = row index, sorted in place
+    after restoring rows and payloads from pristine device copies. As there,
+    the restore copies are part of the timed step."""
+    from rccl_amd import record_sort as rs
+    from rccl_amd import thrust
+
+    n, arity = workloads.RECORD_SORT_ROWS, 4
+    ex = thrust.Program.load(0).par(torch.cuda.current_stream(0))
+    launch = ex.launch()
+    src_rows = wd.record_rows(arity, n)
+    src_pay = torch.arange(n, dtype=torch.int64, device="cuda")
+    rows = rs.RowBuffer(_buffer(torch, DeviceBuffer, src_rows.clone(), np.uint32), arity, n)
+    pay = _buffer(torch, DeviceBuffer, src_pay.clone(), np.uint64)
+    ws_bytes = abi.workspace_bytes("rccl_hip_record_sort_workspace_bytes", arity, 8, n)
+    ws = DeviceBuffer.bytes(ws_bytes)
+    lib = abi.load()
+
+    def step():
+        rows.words.tensor.copy_(src_rows)
+        pay.tensor.copy_(src_pay)
+        abi.check(lib.rccl_hip_record_sort(arity, 8, rows.ptr, pay.ptr, rows.ptr, pay.ptr, n,
+                                           ws.ptr, ws_bytes, launch.handle))
+
+    ms, ms_min, wall, kms, launches, per_step = time_steps(torch, abi, launch.stream(), steps,
+                                                           warmup, step)
+    host_rows = workloads.record_rows(arity, n)
+    order = np.lexsort(host_rows.T[::-1])  # stable: equal rows keep index order
+    ok = bool(np.array_equal(rows.to_host_vec(), host_rows[order]))
+    ok = ok and bool(np.array_equal(pay.to_host_vec(), order.astype(np.uint64)))
+    # Byte positions in pass order (last column's low byte first) that vary
+    # across the rows: the passes the library runs (an in-place sort with an
+    # odd count also runs the first constant one).
+    varying = [bool(np.any(((host_rows[:, arity - 1 - p // 4] >> (8 * (p % 4))) & 0xFF)
+                           != ((host_rows[0, arity - 1 - p // 4] >> (8 * (p % 4))) & 0xFF)))
+               for p in range(4 * arity)]
+    if sum(varying) % 2:
+        varying[varying.index(False)] = True
+    active = [i for i, v in enumerate(varying) if v]
+    sweeps = [[kms_ for name, kms_ in st if name == "record_onesweep"] for st in per_step]
+    active_ms = [sw[i] for sw in sweeps for i in active]
+    idle_ms = [sw[i] for sw in sweeps for i in range(len(sw)) if i not in active]
+    onesweep_ms = sum(active_ms) / len(active_ms)
+    sort_ms = sum(k for st in per_step for name, k in st) / len(per_step)
+    res = {
+        "workload": f"record sort: {n} rows of [u32; 4] (reference generator), u64 payload = "
+                    "row index, in place after a device-to-device restore (both timed, as in "
+                    "the reference benchmark)",
+        "value": round(n / (ms * 1e-3) / 1e6, 2), "unit": "Mrows/s",
+        "ms_per_step": round(ms, 4), "ms_per_step_min": round(ms_min, 4),
+        "ms_per_step_wall": round(wall, 4), "sort_kernels_ms": round(sort_ms, 4),
+        "active_passes": len(active), "passes": 4 * arity,
+        "bytes_model": f"24 B/row moved: 48 B/row restore copies + 16 B/row histogram read + "
+                       f"48 B/row per active onesweep pass ({len(active)} of {4 * arity})",
+        "reference_published_ms": {"rccl_sm89": 0.437555, "cub_sm89": 0.445030,
+                                   "source": "SRDATALOG_HISA_RCCL_TODO.md:180 (other hardware)"},
+        "roofline": roofline(48.0 * n, onesweep_ms,
+                             "record_onesweep, active passes (24 B/row read + 24 B/row write)"),
+        "idle_pass_ms": round(sum(idle_ms) / max(len(idle_ms), 1), 4),
+        "kernel_ms": _rounded(kms), "validated": ok,
+    }
+    del src_rows, src_pay, rows, pay, ws
+    torch.cuda.empty_cache()
+    return res
 
 
 def main():
@@ -433,7 +511,12 @@ def main():
         _log("C5 set operations")
         so = run_set_ops(torch, np, cub, abi, DeviceBuffer, wd, log_sort, args.steps, args.warmup)
         _log("C5 set operations done")
-        out["ordering"] = {"merge": mg, "merge_sort": ms, "set_ops": so}
+        _log("record sort")
+        rsr = run_record_sort(torch, np, abi, DeviceBuffer, wd, workloads, args.steps,
+                              args.warmup)
+        _log(f"record sort: {rsr['ms_per_step']:.3f} ms")
+        out["ordering"] = {"merge": mg, "merge_sort": ms, "set_ops": so, "record_sort": rsr}
+        valid = valid and rsr["validated"]
         valid = valid and mg["validated"] and ms["validated"] and all(
             so[op]["validated"] for op in ("union", "intersection", "difference",
                                            "symmetric_difference"))

@@ -223,6 +223,35 @@ RCCL_HIP_API rccl_hip_status rccl_hip_merge_sort(rccl_hip_key_kind key, size_t v
                                     size_t workspace_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Record sort (SRDatalog/HISA relation rows)
+ * ------------------------------------------------------------------------ */
+
+/* Workspace bytes for a record sort of n rows of `arity` u32 columns with a
+ * payload of payload_bytes (0, 1 or 8) per row. Replaces the internal
+ * DeviceMergeSort{Keys,Pairs}Workspace of the record sorts
+ * (rccl-thrust/src/record_sort.rs:159-160,253-254). UNSUPPORTED_TARGET for an
+ * arity outside 2..6 (record_sort.rs:117-126). */
+RCCL_HIP_API rccl_hip_status rccl_hip_record_sort_workspace_bytes(uint32_t arity,
+                                                     size_t payload_bytes, size_t n,
+                                                     size_t *bytes);
+
+/* Stable ascending lexicographic sort of n padding-free rows of `arity` u32
+ * columns (row-major, 4 * arity bytes per row); equal rows keep their input
+ * order, and each row's payload (payload_bytes = 0, 1 for BooleanProvenance or
+ * 8 for u64/f64, NULL pointers when 0) moves with it. in_rows == out_rows
+ * (and in_payloads == out_payloads) sorts in place; otherwise the inputs are
+ * left untouched; inputs and outputs must otherwise not overlap. From 65,536
+ * rows the sort is a multi-word LSD radix sort whose ranking relies on the
+ * check rccl_hip_program_load runs, so load the device first. Replaces
+ * sort_rows_lexicographic{,_into} and sort_rows_with_payload_lexicographic{,_into}
+ * (rccl-thrust/src/record_sort.rs:144-366). */
+RCCL_HIP_API rccl_hip_status rccl_hip_record_sort(uint32_t arity, size_t payload_bytes,
+                                     const void *in_rows, const void *in_payloads,
+                                     void *out_rows, void *out_payloads, size_t n,
+                                     void *workspace, size_t workspace_bytes,
+                                     hipStream_t stream);
+
+/* ------------------------------------------------------------------------
  * Set operations
  * ------------------------------------------------------------------------ */
 

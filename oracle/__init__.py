@@ -67,6 +67,9 @@ def _load():
         lib.oracle_set_op.argtypes = [c.c_int, c.c_int, c.c_int, c.c_void_p, c.c_void_p,
                                       c.c_size_t, c.c_void_p, c.c_void_p, c.c_size_t,
                                       c.c_void_p, c.c_void_p, c.c_size_t]
+        lib.oracle_record_sort.restype = c.c_int
+        lib.oracle_record_sort.argtypes = [c.c_uint, c.c_void_p, c.c_void_p, c.c_size_t,
+                                           c.c_size_t]
         lib.oracle_sort_unstable_u32.restype = c.c_int
         lib.oracle_sort_unstable_u32.argtypes = [c.c_void_p, c.c_size_t]
         lib.oracle_par_sort_unstable_u32.restype = c.c_int
@@ -178,3 +181,15 @@ def par_sort_unstable_u32(keys, threads):
     if _load().oracle_par_sort_unstable_u32(_ptr(k), k.size, int(threads)) != 0:
         raise ValueError("oracle_par_sort_unstable_u32 failed")
     return k
+
+
+def record_sort(rows, payloads=None):
+    """Stable ascending lexicographic sort of a copy of `rows` (an (n, arity)
+    u32 array) and `payloads` (n items or None); returns (rows, payloads)."""
+    r = np.ascontiguousarray(rows, dtype=np.uint32).copy()
+    if r.ndim != 2:
+        raise ValueError("rows must be a 2-D (n, arity) array")
+    p = None if payloads is None else np.ascontiguousarray(payloads).copy()
+    if _load().oracle_record_sort(r.shape[1], _ptr(r), _ptr(p), _vbytes(p), r.shape[0]) != 0:
+        raise ValueError("oracle_record_sort: arity outside 2..6")
+    return r, p

@@ -240,6 +240,44 @@ int oracle_merge_sort(int kind, int descending, void *keys, void *values,
   return 0;
 }
 
+/* Relation-row sort: the reference's record sort
+ * (rccl-thrust/src/record_sort.rs:88-126,144-366) orders [u32; N] rows by the
+ * unrolled unsigned lexicographic comparator (:88-115) with a stable merge
+ * sort, arity 2..6; a payload row moves with its key row. Restated as a
+ * bottom-up stable merge sort of row indices, then a gather. */
+static int row_less(const uint32_t *rows, unsigned arity, size_t x, size_t y) {
+  const uint32_t *a = rows + x * arity, *b = rows + y * arity;
+  for (unsigned c = 0; c < arity; ++c)
+    if (a[c] != b[c]) return a[c] < b[c];
+  return 0;
+}
+
+int oracle_record_sort(unsigned arity, uint32_t *rows, void *payloads, size_t payload_bytes,
+                       size_t n) {
+  if (arity < 2 || arity > 6) return -1;
+  if (n < 2) return 0;
+  size_t *perm = (size_t *)malloc(n * sizeof(size_t));
+  size_t *tmp = (size_t *)malloc(n * sizeof(size_t));
+  for (size_t i = 0; i < n; ++i) perm[i] = i;
+  for (size_t width = 1; width < n; width *= 2) {
+    for (size_t lo = 0; lo < n; lo += 2 * width) {
+      size_t mid = lo + width < n ? lo + width : n;
+      size_t hi = lo + 2 * width < n ? lo + 2 * width : n;
+      size_t i = lo, j = mid, o = lo;
+      while (i < mid || j < hi) {
+        int take_right = (i == mid) || (j < hi && row_less(rows, arity, perm[j], perm[i]));
+        tmp[o++] = take_right ? perm[j++] : perm[i++];
+      }
+    }
+    size_t *t = perm; perm = tmp; tmp = t;
+  }
+  gather(rows, (size_t)arity * sizeof(uint32_t), perm, n);
+  gather(payloads, payload_bytes, perm, n);
+  free(perm);
+  free(tmp);
+  return 0;
+}
+
 /* Sorted multiset operations: the reference's own host oracle
  * rccl-thrust/examples/set_operations_tests.rs:40-107 (host_set_by), whose
  * selections match the serial device operations of

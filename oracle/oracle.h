@@ -82,6 +82,12 @@ long long oracle_set_op(int op, int kind, int descending, const void *a_keys,
                         const void *b_values, size_t nb, void *out_keys,
                         void *out_values, size_t value_bytes);
 
+/* Stable ascending lexicographic sort of n rows of `arity` u32 columns
+ * (row-major), each row's payload (payload_bytes, may be 0) moving with it.
+ * Returns 0, or -1 for an arity outside 2..6. */
+int oracle_record_sort(unsigned arity, uint32_t *rows, void *payloads,
+                       size_t payload_bytes, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,6 +55,8 @@ EXPORTED_SYMBOLS = (
     "rccl_hip_merge_sort",
     "rccl_hip_set_op_workspace_bytes",
     "rccl_hip_set_op",
+    "rccl_hip_record_sort_workspace_bytes",
+    "rccl_hip_record_sort",
 )
 
 
@@ -153,6 +155,10 @@ def _declare(lib):
     lib_view.rccl_hip_merge_sort_workspace_bytes.argtypes = [st, sz, sz, c.POINTER(sz)]
     lib_view.rccl_hip_merge_sort.restype = st
     lib_view.rccl_hip_merge_sort.argtypes = [st, sz, st, vp, vp, vp, vp, sz, vp, sz, vp]
+    lib_view.rccl_hip_record_sort_workspace_bytes.restype = st
+    lib_view.rccl_hip_record_sort_workspace_bytes.argtypes = [c.c_uint32, sz, sz, c.POINTER(sz)]
+    lib_view.rccl_hip_record_sort.restype = st
+    lib_view.rccl_hip_record_sort.argtypes = [c.c_uint32, sz, vp, vp, vp, vp, sz, vp, sz, vp]
     lib_view.rccl_hip_set_op_workspace_bytes.restype = st
     lib_view.rccl_hip_set_op_workspace_bytes.argtypes = [st, st, sz, sz, sz, c.POINTER(sz)]
     lib_view.rccl_hip_set_op.restype = st

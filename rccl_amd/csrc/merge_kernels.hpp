@@ -90,12 +90,13 @@ __device__ __forceinline__ void merge_tile(MergeSmem<K, V, ITEMS> &sm, const K *
   uint32_t ib = d - ia;
   K outk[ITEMS];
   uint32_t src[PAIRS ? ITEMS : 1];
+  using ordering::pick;
   K ka = ia < la ? sm.keys[ia] : K{};
   K kb = ib < lb ? sm.keys[la + ib] : K{};
 #pragma unroll
   for (int k = 0; k < ITEMS; ++k) {
     const bool take_b = ib < lb && (ia >= la || less(kb, ka));
-    outk[k] = take_b ? kb : ka;
+    outk[k] = pick(take_b, kb, ka);
     if constexpr (PAIRS) src[k] = take_b ? la + ib : ia;
     if (take_b) {
       ++ib;

@@ -24,6 +24,14 @@ struct Less {
   }
 };
 
+// Choice between two keys. Aggregate keys (record rows) overload it in their
+// own namespace with a per-word choice, found by argument-dependent lookup, so
+// the choice stays in registers instead of selecting between stack addresses.
+template <class K>
+__device__ __forceinline__ K pick(bool c, const K &x, const K &y) {
+  return c ? x : y;
+}
+
 template <class T>
 __device__ __forceinline__ T load_or(const T *p, size_t i, size_t n, T fallback) {
   return i < n ? p[i] : fallback;

@@ -465,13 +465,25 @@ __device__ __forceinline__ Desc lookback_consume(const LookbackBuf<Desc> &lbuf, 
   return excl;
 }
 
+// Opaque copy: the compiler must assume the value changed here, so it cannot
+// carry values derived from it across this point. Aggregate keys (record
+// rows) overload it in their own namespace, found by argument-dependent
+// lookup.
+template <class T>
+__device__ __forceinline__ void launder(T &x) {
+  asm volatile("" : "+v"(x));
+}
+
+// One tile of a onesweep pass. Keys are any trivially copyable type whose
+// digits Ops::digit extracts (scalar keys, or record rows); the kernels below
+// wrap it.
 template <class Bits, class Val, class Ops, int ITEMS, class Desc, int THREADS>
-__global__ void __launch_bounds__(THREADS, RCCL_RADIX_WAVES_PER_SIMD)
-onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
-                const Val *__restrict__ vals_in, Val *__restrict__ vals_out, size_t n,
-                uint32_t num_tiles, const uint32_t *__restrict__ pass_bins,
-                LookbackBuf<Desc> lbuf, LookbackBuf<Desc> lbuf_next, uint32_t bit,
-                uint32_t mask) {
+__device__ __forceinline__ void
+onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
+              const Val *__restrict__ vals_in, Val *__restrict__ vals_out, size_t n,
+              uint32_t num_tiles, const uint32_t *__restrict__ pass_bins,
+              LookbackBuf<Desc> lbuf, LookbackBuf<Desc> lbuf_next, uint32_t bit,
+              uint32_t mask) {
   constexpr bool PAIRS = !std::is_same<Val, NoValue>::value;
   constexpr int WAVES = THREADS / 64;
   constexpr int TILE = THREADS * ITEMS;
@@ -596,7 +608,7 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   // consecutive positions in lane order, which with the item loop and the
   // per-wave counters is source order; dummies all land in the spare slot.
 #pragma unroll
-  for (int j = 0; j < ITEMS; ++j) asm volatile("" : "+v"(key[j]));
+  for (int j = 0; j < ITEMS; ++j) launder(key[j]);
   // All atomics are issued before the first staging write, so the round
   // trips overlap; the opaque copy of the positions keeps the compiler from
   // pairing each write with its atomic (which serialises them).
@@ -673,6 +685,18 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
       lbuf_next.gagg[size_t(group) * BINS + tid] = 0;
     }
   }
+}
+
+template <class Bits, class Val, class Ops, int ITEMS, class Desc, int THREADS>
+__global__ void __launch_bounds__(THREADS, RCCL_RADIX_WAVES_PER_SIMD)
+onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
+                const Val *__restrict__ vals_in, Val *__restrict__ vals_out, size_t n,
+                uint32_t num_tiles, const uint32_t *__restrict__ pass_bins,
+                LookbackBuf<Desc> lbuf, LookbackBuf<Desc> lbuf_next, uint32_t bit,
+                uint32_t mask) {
+  onesweep_tile<Bits, Val, Ops, ITEMS, Desc, THREADS>(keys_in, keys_out, vals_in, vals_out, n,
+                                                      num_tiles, pass_bins, lbuf, lbuf_next, bit,
+                                                      mask);
 }
 
 // ---------------------------------------------------------------------------

@@ -217,3 +217,16 @@ def c5_inputs(n_each: int = 1 << 26):
     a = _c5_side(pool, SEEDS["C5a"], n_each)
     b = _c5_side(pool, SEEDS["C5b"], n_each)
     return a, b
+
+
+def record_rows(arity: int, n: int) -> np.ndarray:
+    """Relation rows of the reference's record-sort example and benchmark
+    (rccl-thrust/examples/record_sort.rs:11-23, record_sort_benchmark.rs:33-39):
+    row[i][c] = (i * (6c + 5) + 3c) mod (11 + 2c), an (n, arity) u32 array."""
+    idx = np.arange(n, dtype=np.uint64)[:, None]
+    col = np.arange(arity, dtype=np.uint64)[None, :]
+    return ((idx * (col * _U64(6) + _U64(5)) + col * _U64(3)) % (_U64(11) + col * _U64(2))).astype(
+        np.uint32)
+
+
+RECORD_SORT_ROWS = (1 << 20) + 13  # record_sort_benchmark.rs:4

@@ -108,3 +108,10 @@ def c5_inputs(n_each: int = 1 << 26, device="cuda"):
     pool = hash_range(SEEDS["C5_pool"], n_each, device=device)
     return _c5_side(pool, SEEDS["C5a"], n_each, device), _c5_side(pool, SEEDS["C5b"], n_each,
                                                                    device)
+
+
+def record_rows(arity: int, n: int, device="cuda") -> torch.Tensor:
+    """Device twin of workloads.record_rows, flattened row-major as int32."""
+    idx = torch.arange(n, dtype=torch.int64, device=device)[:, None]
+    col = torch.arange(arity, dtype=torch.int64, device=device)[None, :]
+    return ((idx * (col * 6 + 5) + col * 3) % (11 + col * 2)).to(torch.int32).reshape(-1)

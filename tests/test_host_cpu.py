@@ -109,6 +109,72 @@ def test_set_validation(lib):
                                FAKE, 1 << 20, None) == 9
 
 
+def test_record_sort_validation(lib):
+    out = ctypes.c_size_t()
+    # Arity 2..6 only (rccl-thrust/src/record_sort.rs:117-126).
+    for arity in (0, 1, 7):
+        assert lib.rccl_hip_record_sort_workspace_bytes(arity, 0, 10, ctypes.byref(out)) == 4
+        info = _last()
+        assert b"arities 2 through 6" in info.role and b"use radix sort" in info.role
+        assert lib.rccl_hip_record_sort(arity, 0, FAKE, None, FAKE, None, 10, FAKE, 1 << 20,
+                                        None) == 4
+    # Payloads are u64/f64 (8 bytes) or BooleanProvenance (1 byte).
+    for width in (2, 4, 16):
+        assert lib.rccl_hip_record_sort_workspace_bytes(3, width, 10, ctypes.byref(out)) == 9
+    need = _abi.workspace_bytes("rccl_hip_record_sort_workspace_bytes", 4, 8, 100_000)
+    assert need >= 100_000 * (16 + 8)  # scratch rows and payloads
+    assert lib.rccl_hip_record_sort(4, 8, FAKE, FAKE, FAKE, FAKE, 100_000, FAKE, need - 1,
+                                    None) == 2
+    assert (_last().expected, _last().actual) == (need, need - 1)
+    assert lib.rccl_hip_record_sort(4, 8, FAKE, None, FAKE, FAKE, 10, FAKE, need, None) == 9
+    assert lib.rccl_hip_record_sort(4, 0, None, None, None, None, 0, None, 0, None) == 0
+    for arity in range(2, 7):
+        small = _abi.workspace_bytes("rccl_hip_record_sort_workspace_bytes", arity, 0, 1000)
+        assert small >= 1000 * 4 * arity
+
+
+def test_record_sort_contract_errors_before_device_work():
+    """The reference's contract errors (rccl-thrust/examples/record_sort.rs:164-201),
+    raised before any buffer is touched, so host tensors stand in for device ones."""
+    import torch
+
+    from rccl_amd import record_sort as rs
+    from rccl_amd.device import DeviceBuffer
+
+    def rows(arity, n):
+        return rs.RowBuffer(DeviceBuffer(torch.zeros(max(arity * n, 1), dtype=torch.int32),
+                                         np.uint32, arity * n), arity, n)
+
+    def buf(dtype, n):
+        return DeviceBuffer(torch.zeros(max(n, 1), dtype=torch.int64), dtype, n)
+
+    ex = None  # never reached: validation fails first
+    with pytest.raises(_abi.DeviceAlgorithmError, match="record-sort payload"):
+        rs.sort_rows_with_payload_lexicographic(ex, rows(2, 3), buf(np.uint64, 2))
+    with pytest.raises(_abi.DeviceAlgorithmError, match="record-sort output"):
+        rs.sort_rows_lexicographic_into(ex, rows(2, 3), rows(2, 2))
+    with pytest.raises(_abi.DeviceAlgorithmError, match="output payload"):
+        rs.sort_rows_with_payload_lexicographic_into(ex, rows(2, 3), buf(np.uint64, 3),
+                                                     rows(2, 3), buf(np.uint64, 2))
+    with pytest.raises(_abi.DeviceAlgorithmError, match="output rows"):
+        rs.sort_rows_with_payload_lexicographic_into(ex, rows(2, 3), buf(np.uint64, 3),
+                                                     rows(2, 4), buf(np.uint64, 3))
+    with pytest.raises(_abi.DeviceAlgorithmError, match="input payload"):
+        rs.sort_rows_with_payload_lexicographic_into(ex, rows(2, 3), buf(np.uint64, 4),
+                                                     rows(2, 3), buf(np.uint64, 3))
+    with pytest.raises(_abi.DeviceAlgorithmError, match="use radix sort for scalar keys") as e:
+        rs.sort_rows_lexicographic(ex, rows(1, 3))
+    assert e.value.kind == "UnsupportedTarget"
+    with pytest.raises(_abi.DeviceAlgorithmError, match="arities 2 through 6"):
+        rs.sort_rows_lexicographic(ex, rows(7, 1))
+    # Arity is checked before lengths, as in the reference.
+    with pytest.raises(_abi.DeviceAlgorithmError, match="arities 2 through 6"):
+        rs.sort_rows_with_payload_lexicographic(ex, rows(7, 3), buf(np.uint64, 2))
+    # Only the sealed payload set is accepted.
+    with pytest.raises(TypeError):
+        rs.sort_rows_with_payload_lexicographic(ex, rows(2, 3), buf(np.uint32, 3))
+
+
 def test_workspace_sizes_scale(lib):
     small = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", 0, 0, 1 << 10)
     big = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", 0, 0, 1 << 28)

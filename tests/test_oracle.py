@@ -48,6 +48,15 @@ def _golden_cases():
 
 @pytest.mark.parametrize("case", _golden_cases(), ids=lambda c: c["id"])
 def test_oracle_reproduces_reference_vectors(case):
+    if case["op"] == "record_sort":
+        rows = np.array(case["rows"], dtype=np.uint32)
+        pay = None if "payloads" not in case else np.array(case["payloads"],
+                                                          dtype=NP[case["payload_dtype"]])
+        out_rows, out_pay = oracle.record_sort(rows, pay)
+        assert out_rows.tolist() == case["expected_rows"]
+        if "expected_payloads" in case:
+            assert out_pay.tolist() == case["expected_payloads"]
+        return
     kind, desc = case["kind"], case["descending"]
     vdt = NP.get(case.get("value_dtype", ""), None)
     if case["op"] == "radix_sort":
@@ -314,3 +323,34 @@ def test_cpu_baseline_sorts_vs_numpy(n, threads):
     want = np.sort(keys)
     assert np.array_equal(oracle.sort_unstable_u32(keys), want)
     assert np.array_equal(oracle.par_sort_unstable_u32(keys, threads), want)
+
+
+def _reference_rows(arity, n):
+    """The row generator of rccl-thrust/examples/record_sort.rs:11-23."""
+    idx = np.arange(n, dtype=np.int64)[:, None]
+    col = np.arange(arity, dtype=np.int64)[None, :]
+    return ((idx * (col * 6 + 5) + col * 3) % (11 + col * 2)).astype(np.uint32)
+
+
+@pytest.mark.parametrize("arity", [2, 3, 4, 5, 6])
+@pytest.mark.parametrize("n", [0, 1, 31, 257, 10003])
+def test_record_sort_oracle_vs_lexsort(arity, n):
+    """Row sort against numpy's stable lexsort (last key primary) on the
+    reference's row generator and on random rows over a small alphabet, with
+    the input index as payload so stability is visible."""
+    rng = np.random.default_rng(arity * 1000 + n)
+    for rows in (_reference_rows(arity, n),
+                 rng.integers(0, 3, size=(n, arity), dtype=np.uint64).astype(np.uint32),
+                 rng.integers(0, 1 << 32, size=(n, arity), dtype=np.uint64).astype(np.uint32)):
+        pay = np.arange(n, dtype=np.uint64)
+        order = np.lexsort(rows.T[::-1]) if n else np.arange(0)
+        out_rows, out_pay = oracle.record_sort(rows, pay)
+        assert np.array_equal(out_rows, rows[order])
+        assert np.array_equal(out_pay, pay[order])
+
+
+def test_record_sort_oracle_rejects_arity():
+    with pytest.raises(ValueError):
+        oracle.record_sort(np.zeros((3, 1), dtype=np.uint32))
+    with pytest.raises(ValueError):
+        oracle.record_sort(np.zeros((3, 7), dtype=np.uint32))
