@@ -282,6 +282,22 @@ RCCL_HIP_API rccl_hip_status rccl_hip_set_op(rccl_hip_set_operation op, rccl_hip
                                 uint64_t *d_out_count, void *workspace,
                                 size_t workspace_bytes, hipStream_t stream);
 
+/* Set operation over two finite arithmetic ranges, keys only: item i of A is
+ * a_start + a_step * i (and likewise B), in the key type's wrapping integer
+ * arithmetic; neither input is materialised. a_start/a_step/b_start/b_step
+ * point to one host value of the key type each. Integer key kinds only; each
+ * index must fit the key type (the reference traps on the device when it does
+ * not; here the call fails before any launch). Output, count, capacity and
+ * workspace (rccl_hip_set_op_workspace_bytes with value_bytes 0) as for
+ * rccl_hip_set_op. Replaces Launch::set_arithmetic
+ * (rccl-cub/src/dispatch.rs:552-740, set_operation.rs:417-480) and the Thrust
+ * arithmetic-range expressions (rccl-thrust/src/set.rs:127-244,477-530). */
+RCCL_HIP_API rccl_hip_status rccl_hip_set_op_arithmetic(
+    rccl_hip_set_operation op, rccl_hip_key_kind key, rccl_hip_order order,
+    const void *a_start, const void *a_step, size_t na, const void *b_start,
+    const void *b_step, size_t nb, void *out_keys, size_t out_capacity, uint64_t *d_out_count,
+    void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

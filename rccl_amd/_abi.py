@@ -55,6 +55,7 @@ EXPORTED_SYMBOLS = (
     "rccl_hip_merge_sort",
     "rccl_hip_set_op_workspace_bytes",
     "rccl_hip_set_op",
+    "rccl_hip_set_op_arithmetic",
     "rccl_hip_record_sort_workspace_bytes",
     "rccl_hip_record_sort",
 )
@@ -164,6 +165,9 @@ def _declare(lib):
     lib_view.rccl_hip_set_op.restype = st
     lib_view.rccl_hip_set_op.argtypes = [st, st, sz, st, vp, vp, sz, vp, vp, sz, vp, vp, sz, vp, vp,
                                          sz, vp]
+    lib_view.rccl_hip_set_op_arithmetic.restype = st
+    lib_view.rccl_hip_set_op_arithmetic.argtypes = [st, st, st, vp, vp, sz, vp, vp, sz, vp, sz, vp,
+                                                    vp, sz, vp]
 
 
 def load():

@@ -1,5 +1,7 @@
 // Set operation C ABI: validation (before any launch) and dispatch of the
 // runtime key kind onto the per-kind instantiations in set_<kind>.hip.
+#include <cstring>
+
 #include "set_ops_kernels.hpp"
 
 using namespace rccl_hip;
@@ -56,6 +58,23 @@ rccl_hip_status set_run(rccl_hip_key_kind key, const set_ops::SetArgs &s, size_t
   return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "set key kind");
 }
 
+// Largest index an arithmetic range of `key` can address: the reference converts
+// each index to the key type and traps when it does not fit
+// (rccl-cub/src/ordering_backend/set.rs:72-80).
+uint64_t max_arith_index(rccl_hip_key_kind key) {
+  switch (key) {
+  case RCCL_HIP_KEY_U8: return 0xFFu;
+  case RCCL_HIP_KEY_I8: return 0x7Fu;
+  case RCCL_HIP_KEY_U16: return 0xFFFFu;
+  case RCCL_HIP_KEY_I16: return 0x7FFFu;
+  case RCCL_HIP_KEY_U32: return 0xFFFFFFFFu;
+  case RCCL_HIP_KEY_I32: return 0x7FFFFFFFu;
+  case RCCL_HIP_KEY_U64: return ~0ull;
+  case RCCL_HIP_KEY_I64: return 0x7FFFFFFFFFFFFFFFull;
+  default: return 0;  // floating keys have no arithmetic ranges
+  }
+}
+
 } // namespace
 
 extern "C" {
@@ -102,6 +121,50 @@ rccl_hip_status rccl_hip_set_op(rccl_hip_set_operation op, rccl_hip_key_kind key
   s.ws_bytes = workspace_bytes;
   s.stream = stream;
   return set_run(key, s, vb, order == RCCL_HIP_ORDER_DESCENDING);
+}
+
+rccl_hip_status rccl_hip_set_op_arithmetic(rccl_hip_set_operation op, rccl_hip_key_kind key,
+                                           rccl_hip_order order, const void *a_start,
+                                           const void *a_step, size_t na, const void *b_start,
+                                           const void *b_step, size_t nb, void *out_keys,
+                                           size_t out_capacity, uint64_t *d_out_count,
+                                           void *workspace, size_t workspace_bytes,
+                                           hipStream_t stream) {
+  RCCL_HIP_TRY(checks(op, key, 0, order, na, nb));
+  if (key == RCCL_HIP_KEY_F32 || key == RCCL_HIP_KEY_F64)
+    return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "arithmetic range key kind");
+  if ((na && (!a_start || !a_step)) || (nb && (!b_start || !b_step)))
+    return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "arithmetic range start or step");
+  const uint64_t max_index = max_arith_index(key);
+  if (na > 0 && uint64_t(na - 1) > max_index)
+    return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "first arithmetic range index",
+                     max_index + 1, na);
+  if (nb > 0 && uint64_t(nb - 1) > max_index)
+    return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "second arithmetic range index",
+                     max_index + 1, nb);
+  if (!out_keys && !d_out_count)
+    return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "set output count");
+  set_ops::SetArgs s{};
+  s.op = static_cast<int>(op);
+  s.na = na;
+  s.nb = nb;
+  s.out = out_keys;
+  s.out_cap = out_keys ? out_capacity : 0;
+  s.out_count = d_out_count;
+  s.ws = workspace;
+  s.ws_bytes = workspace_bytes;
+  s.stream = stream;
+  s.arith = true;
+  const size_t kb = key_bytes(key);
+  if (na) {
+    std::memcpy(&s.a_start, a_start, kb);
+    std::memcpy(&s.a_step, a_step, kb);
+  }
+  if (nb) {
+    std::memcpy(&s.b_start, b_start, kb);
+    std::memcpy(&s.b_step, b_step, kb);
+  }
+  return set_run(key, s, 0, order == RCCL_HIP_ORDER_DESCENDING);
 }
 
 } // extern "C"

@@ -16,6 +16,7 @@
 #pragma once
 
 #include <algorithm>
+#include <cstring>
 
 #include "ordering_common.hpp"
 
@@ -45,6 +46,25 @@ constexpr uint64_t F_AGG = 1ull << 62, F_INCL = 2ull << 62, VMASK = (1ull << 62)
 // Group aggregate: tiles counted in the top 16 bits, count below.
 constexpr int GA_SHIFT = 48;
 constexpr uint64_t GA_MASK = (1ull << GA_SHIFT) - 1;
+
+// Finite arithmetic input range: item i is start + step * i in the key's own
+// wrapping integer arithmetic (rccl-cub/src/ordering_backend/set.rs:49-81,
+// rccl-cub/src/range.rs:43-78); nothing is materialised. Indices are checked
+// on the host to fit the key type.
+template <class K>
+struct Arith {
+  K start, step;
+};
+template <class K>
+__device__ __forceinline__ K arith_at(const Arith<K> &r, size_t i) {
+  if constexpr (std::is_integral<K>::value) {
+    using W = typename std::conditional<(sizeof(K) <= 4), uint32_t, uint64_t>::type;
+    return static_cast<K>(static_cast<W>(static_cast<W>(r.start) +
+                                         static_cast<W>(r.step) * static_cast<W>(i)));
+  } else {
+    return K{};  // arithmetic ranges are integral only
+  }
+}
 
 // Balanced path at `diag` (rccl-cub/src/ordering_backend/set.rs:436-506): the
 // merge-path split, moved inside a run of keys equal to B[j] so that the run's
@@ -98,16 +118,21 @@ __device__ __forceinline__ void balanced_path(RA a, size_t na, RB b, size_t nb, 
   out_j = diag - i + star;
 }
 
-template <class K, class Cmp>
+template <class K, class Cmp, bool ARITH>
 __global__ void __launch_bounds__(256)
 partition_kernel(const K *__restrict__ a, size_t na, const K *__restrict__ b, size_t nb,
-                 size_t tile, size_t count, uint64_t *__restrict__ splits) {
+                 size_t tile, size_t count, uint64_t *__restrict__ splits, Arith<K> ar,
+                 Arith<K> br) {
   const size_t t = size_t(blockIdx.x) * 256 + threadIdx.x;
   if (t >= count) return;
   const size_t diag = std::min(t * tile, na + nb);
   size_t i, j;
-  balanced_path<K>([&](size_t x) { return a[x]; }, na, [&](size_t x) { return b[x]; }, nb, diag,
-                   Cmp{}, i, j);
+  if constexpr (ARITH)
+    balanced_path<K>([&](size_t x) { return arith_at(ar, x); }, na,
+                     [&](size_t x) { return arith_at(br, x); }, nb, diag, Cmp{}, i, j);
+  else
+    balanced_path<K>([&](size_t x) { return a[x]; }, na, [&](size_t x) { return b[x]; }, nb,
+                     diag, Cmp{}, i, j);
   splits[2 * t] = i;
   splits[2 * t + 1] = j;
 }
@@ -181,13 +206,13 @@ __device__ __forceinline__ void serial_step(const K &ka, const K &kb, bool a_ok,
   adv_b = live && !a_sel;
 }
 
-template <class K, class V, class Cmp, int OP, int ITEMS>
+template <class K, class V, class Cmp, int OP, int ITEMS, bool ARITH>
 __global__ void __launch_bounds__(THREADS)
 tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restrict__ b,
             const V *__restrict__ bv, const uint64_t *__restrict__ splits, size_t tiles,
             K *__restrict__ out, V *__restrict__ outv, size_t out_cap,
             uint64_t *__restrict__ out_count, uint64_t *desc, uint64_t *gagg, uint64_t *ginc,
-            uint32_t *ticket) {
+            uint32_t *ticket, Arith<K> ar, Arith<K> br) {
   using Smem = TileSmem<K, V, ITEMS>;
   constexpr bool PAIRS = Smem::PAIRS;
   constexpr bool VALS_B = PAIRS && (OP == UNION || OP == SYMMETRIC_DIFFERENCE);
@@ -219,7 +244,10 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
     for (int k = 0; k < STAGE; ++k) {
       const uint32_t i = min(uint32_t(k) * THREADS + tid, len ? len - 1u : 0u);
       const bool from_a = i < la;
-      kr[k] = len ? *(from_a ? a + i0 + i : b + j0 + (i - la)) : K{};
+      if constexpr (ARITH)
+        kr[k] = len ? (from_a ? arith_at(ar, i0 + i) : arith_at(br, j0 + (i - la))) : K{};
+      else
+        kr[k] = len ? *(from_a ? a + i0 + i : b + j0 + (i - la)) : K{};
       if constexpr (PAIRS) {
         if constexpr (VALS_B) vr[k] = len ? *(from_a ? av + i0 + i : bv + j0 + (i - la)) : V{};
         else vr[k] = from_a ? av[i0 + i] : V{};
@@ -408,6 +436,10 @@ struct SetArgs {
   void *ws;
   size_t ws_bytes;
   hipStream_t stream;
+  // Arithmetic inputs (keys only): a and b are unused; start and step hold
+  // the key's bytes in their low bytes.
+  bool arith;
+  uint64_t a_start, a_step, b_start, b_step;
 };
 
 struct Layout {
@@ -459,21 +491,50 @@ rccl_hip_status run_op(const SetArgs &s) {
                    256, 0, s.stream>>>(desc, state_words);
   }
   RCCL_HIP_TRY(check_launch("set clear"));
+  const dim3 pgrid(static_cast<uint32_t>((l.tiles + 1 + 255) / 256));
+  const dim3 tgrid(static_cast<uint32_t>(l.tiles));
+  const K *a = static_cast<const K *>(s.a);
+  const K *b = static_cast<const K *>(s.b);
+  const V *av = static_cast<const V *>(s.av);
+  const V *bv = static_cast<const V *>(s.bv);
+  K *out = static_cast<K *>(s.out);
+  V *outv = static_cast<V *>(s.outv);
+  if (s.arith) {
+    if constexpr (std::is_integral<K>::value && std::is_same<V, NoValue>::value) {
+      Arith<K> ar, br;
+      std::memcpy(&ar.start, &s.a_start, sizeof(K));
+      std::memcpy(&ar.step, &s.a_step, sizeof(K));
+      std::memcpy(&br.start, &s.b_start, sizeof(K));
+      std::memcpy(&br.step, &s.b_step, sizeof(K));
+      {
+        KernelTimer t("set_partition", s.stream, l.tiles + 1);
+        partition_kernel<K, Cmp, true><<<pgrid, 256, 0, s.stream>>>(a, s.na, b, s.nb, TILE,
+                                                                     l.tiles + 1, splits, ar, br);
+      }
+      RCCL_HIP_TRY(check_launch("set partition"));
+      {
+        KernelTimer t("set_tile", s.stream, s.na + s.nb);
+        tile_kernel<K, V, Cmp, OP, ITEMS, true><<<tgrid, THREADS, 0, s.stream>>>(
+            a, av, b, bv, splits, l.tiles, out, outv, s.out_cap, s.out_count, desc, gagg, ginc,
+            ticket, ar, br);
+      }
+      return check_launch("set tile");
+    } else {
+      return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "arithmetic range key kind");
+    }
+  }
   {
     KernelTimer t("set_partition", s.stream, l.tiles + 1);
-    partition_kernel<K, Cmp><<<dim3(static_cast<uint32_t>((l.tiles + 1 + 255) / 256)), 256, 0,
-                               s.stream>>>(static_cast<const K *>(s.a), s.na,
-                                           static_cast<const K *>(s.b), s.nb, TILE, l.tiles + 1,
-                                           splits);
+    partition_kernel<K, Cmp, false><<<pgrid, 256, 0, s.stream>>>(a, s.na, b, s.nb, TILE,
+                                                                  l.tiles + 1, splits, Arith<K>{},
+                                                                  Arith<K>{});
   }
   RCCL_HIP_TRY(check_launch("set partition"));
   {
     KernelTimer t("set_tile", s.stream, s.na + s.nb);
-    tile_kernel<K, V, Cmp, OP, ITEMS><<<dim3(static_cast<uint32_t>(l.tiles)), THREADS, 0,
-                                        s.stream>>>(
-        static_cast<const K *>(s.a), static_cast<const V *>(s.av), static_cast<const K *>(s.b),
-        static_cast<const V *>(s.bv), splits, l.tiles, static_cast<K *>(s.out),
-        static_cast<V *>(s.outv), s.out_cap, s.out_count, desc, gagg, ginc, ticket);
+    tile_kernel<K, V, Cmp, OP, ITEMS, false><<<tgrid, THREADS, 0, s.stream>>>(
+        a, av, b, bv, splits, l.tiles, out, outv, s.out_cap, s.out_count, desc, gagg, ginc,
+        ticket, Arith<K>{}, Arith<K>{});
   }
   return check_launch("set tile");
 }

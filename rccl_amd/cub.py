@@ -438,6 +438,55 @@ def device_set_keys(launch, operation, first, second, workspace, output=None, or
             None, order)
 
 
+class ArithmeticRange:
+    """Finite arithmetic input range: item i is start + step * i in the key
+    type's wrapping arithmetic; never materialised (rccl-cub/src/range.rs:43-78)."""
+
+    def __init__(self, start, step, length: int, dtype=None):
+        self.dtype = np.dtype(dtype if dtype is not None else np.asarray(start).dtype)
+        if self.dtype.kind not in "iu":
+            raise TypeError(f"arithmetic ranges have integer items, not {self.dtype}")
+        self.start = np.asarray(start).astype(self.dtype)
+        self.step = np.asarray(step).astype(self.dtype)
+        self._len = int(length)
+
+    def len(self) -> int:
+        return self._len
+
+    def __len__(self) -> int:
+        return self._len
+
+    def to_host_vec(self) -> np.ndarray:
+        """The items, computed on the host in the same wrapping arithmetic."""
+        wide = np.uint64
+        i = np.arange(self._len, dtype=wide)
+        v = self.start.astype(self.dtype).view(f"u{self.dtype.itemsize}").astype(wide) + \
+            self.step.astype(self.dtype).view(f"u{self.dtype.itemsize}").astype(wide) * i
+        return v.astype(f"u{self.dtype.itemsize}").view(self.dtype)
+
+
+def arithmetic_range(start, step, length: int, dtype=None) -> ArithmeticRange:
+    return ArithmeticRange(start, step, length, dtype)
+
+
+def device_set_arithmetic(launch, operation, first: ArithmeticRange, second: ArithmeticRange,
+                          workspace, output=None, order=ascending):
+    """Enqueue a set operation over two arithmetic ranges (keys only);
+    `output=None` only counts (rccl-cub/src/dispatch.rs:552-740)."""
+    if first.dtype != second.dtype:
+        raise TypeError("both arithmetic ranges must have the same item type")
+    kind = _ordering_kind(first.dtype)
+    a0 = np.ascontiguousarray(np.array([first.start, first.step], dtype=first.dtype))
+    b0 = np.ascontiguousarray(np.array([second.start, second.step], dtype=second.dtype))
+    w = first.dtype.itemsize
+    _abi.check(_abi.load().rccl_hip_set_op_arithmetic(
+        SET_OPERATIONS[operation], _abi.KEY_KINDS[kind], order_code(order),
+        a0.ctypes.data, a0.ctypes.data + w, first.len(), b0.ctypes.data, b0.ctypes.data + w,
+        second.len(), None if output is None else output.ptr,
+        0 if output is None else output.len(), workspace.output_count.ptr, workspace.control.ptr,
+        workspace.control_bytes, launch.handle))
+
+
 def device_set_pairs(launch, operation, first_keys, first_values, second_keys, second_values,
                      workspace, output_keys, output_values, order=ascending):
     _set_op(launch, SET_OPERATIONS[operation], first_keys, first_values, second_keys,

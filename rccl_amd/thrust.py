@@ -7,6 +7,7 @@ StarGazerM/rccl tree):
   sort_by, sort_unstable_by (closure)  ordering.rs:13-44  -> stable merge sort
   view().with_values(..)               range.rs:100-163, ordering.rs:96-129
   a.merge(b).write_into(out, exec)     merge.rs:16-247
+  arithmetic_range(..).difference(..)  set.rs:127-244,477-690 (unmaterialised inputs)
   a.union(b).write_into / .count       set.rs:357-898 (also intersection,
                                        difference, symmetric_difference)
 Every call allocates its temporary workspace on the device, runs on the
@@ -159,6 +160,41 @@ class KeyValueRangeMut(KeyValueRange):
     pass
 
 
+class ArithmeticRange(cub.ArithmeticRange):
+    """An unmaterialised arithmetic range with the fluent set operations of
+    ArithmeticSetRangeExt (rccl-thrust/src/set.rs:544-690). Both sides of an
+    expression are arithmetic ranges of the same item type."""
+
+    def union(self, second):
+        return _SetExpression("union", self, second, ascending)
+
+    def union_by(self, second, order):
+        return _SetExpression("union", self, second, order)
+
+    def intersection(self, second):
+        return _SetExpression("intersection", self, second, ascending)
+
+    def intersection_by(self, second, order):
+        return _SetExpression("intersection", self, second, order)
+
+    def difference(self, second):
+        return _SetExpression("difference", self, second, ascending)
+
+    def difference_by(self, second, order):
+        return _SetExpression("difference", self, second, order)
+
+    def symmetric_difference(self, second):
+        return _SetExpression("symmetric_difference", self, second, ascending)
+
+    def symmetric_difference_by(self, second, order):
+        return _SetExpression("symmetric_difference", self, second, order)
+
+
+def arithmetic_range(start, step, length: int, dtype=None) -> ArithmeticRange:
+    """rccl_thrust::arithmetic_range (rccl-cub/src/range.rs:76-78)."""
+    return ArithmeticRange(start, step, length, dtype)
+
+
 def view(buffer: DeviceBuffer) -> DeviceView:
     return DeviceView(buffer)
 
@@ -249,6 +285,18 @@ class _SetExpression:
 
     def _run(self, output, execution: Execution) -> int:
         launch = execution.launch()
+        if isinstance(self.first, cub.ArithmeticRange):
+            # rccl-thrust/src/set.rs:127-244: both sides arithmetic, keys only.
+            if not isinstance(self.second, cub.ArithmeticRange):
+                raise TypeError("an arithmetic range combines with an arithmetic range")
+            if self.first.len() + self.second.len() == 0:
+                return 0
+            ok = None if output is None else _split(output)[0]
+            ws = cub.device_set_workspace(launch, self.operation, self.first.dtype,
+                                          self.first.len(), self.second.len())
+            cub.device_set_arithmetic(launch, self.operation, self.first, self.second, ws, ok,
+                                      self.order)
+            return ws.count()
         ak, av = _split(self.first)
         bk, bv = _split(self.second)
         ok, ov = (None, None) if output is None else _split(output)

@@ -109,6 +109,46 @@ def test_set_validation(lib):
                                FAKE, 1 << 20, None) == 9
 
 
+def test_set_arithmetic_validation(lib):
+    one = ctypes.c_int64(1)
+    p1 = ctypes.byref(one)
+    need = _abi.workspace_bytes("rccl_hip_set_op_workspace_bytes", 0, 4, 0, 300, 300)
+    # Floating keys have no arithmetic ranges.
+    assert lib.rccl_hip_set_op_arithmetic(0, 2, 0, p1, p1, 10, p1, p1, 10, FAKE, 20, FAKE, FAKE,
+                                          need, None) == 9
+    # Every index must fit the key type: u8 holds 256 items, i8 128.
+    assert lib.rccl_hip_set_op_arithmetic(0, 6, 0, p1, p1, 257, p1, p1, 10, FAKE, 300, FAKE,
+                                          FAKE, need, None) == 9
+    info = _last()
+    assert info.role == b"first arithmetic range index" and (info.expected, info.actual) == (
+        256, 257)
+    assert lib.rccl_hip_set_op_arithmetic(0, 7, 0, p1, p1, 10, p1, p1, 129, FAKE, 300, FAKE,
+                                          FAKE, need, None) == 9
+    assert _last().role == b"second arithmetic range index"
+    # Missing start/step, missing output and count, short workspace.
+    assert lib.rccl_hip_set_op_arithmetic(0, 4, 0, None, p1, 10, p1, p1, 10, FAKE, 20, FAKE,
+                                          FAKE, need, None) == 9
+    assert lib.rccl_hip_set_op_arithmetic(0, 4, 0, p1, p1, 10, p1, p1, 10, None, 0, None, FAKE,
+                                          need, None) == 9
+    big = _abi.workspace_bytes("rccl_hip_set_op_workspace_bytes", 0, 4, 0, 1 << 20, 1 << 20)
+    assert lib.rccl_hip_set_op_arithmetic(0, 4, 0, p1, p1, 1 << 20, p1, p1, 1 << 20, FAKE,
+                                          1 << 21, FAKE, FAKE, big - 1, None) == 2
+    # Overflowing combined length.
+    assert lib.rccl_hip_set_op_arithmetic(0, 4, 0, p1, p1, (1 << 64) - 1, p1, p1, 2, FAKE, 1,
+                                          FAKE, FAKE, big, None) == 5
+
+
+def test_arithmetic_range_host_items():
+    r = cub.arithmetic_range(np.uint8(250), np.uint8(3), 4)
+    assert r.to_host_vec().tolist() == [250, 253, 0, 3]  # wrapping u8 arithmetic
+    r = cub.arithmetic_range(np.int16(100), np.int16(-7), 3)
+    assert r.to_host_vec().tolist() == [100, 93, 86]
+    r = cub.arithmetic_range(np.int64(-(1 << 62)), np.int64(1 << 61), 5)
+    assert r.to_host_vec().tolist() == [-(1 << 62) + k * (1 << 61) for k in range(5)]
+    with pytest.raises(TypeError):
+        cub.arithmetic_range(np.float32(0), np.float32(1), 3)
+
+
 def test_record_sort_validation(lib):
     out = ctypes.c_size_t()
     # Arity 2..6 only (rccl-thrust/src/record_sort.rs:117-126).

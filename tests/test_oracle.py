@@ -76,7 +76,10 @@ def test_oracle_reproduces_reference_vectors(case):
         vals = None if "values" not in case else np.array(case["values"], dtype=vdt)
         out = oracle.merge_sort(kind, keys, vals, desc)
     else:
-        a, b = _keys(case, "a", kind), _keys(case, "b", kind)
+        if "a_range" in case:  # arithmetic ranges: materialised here for the oracle
+            a, b = _arith(case["a_range"], kind), _arith(case["b_range"], kind)
+        else:
+            a, b = _keys(case, "a", kind), _keys(case, "b", kind)
         av = None if "a_values" not in case else np.array(case["a_values"], vdt)
         bv = None if "b_values" not in case else np.array(case["b_values"], vdt)
         out = oracle.set_op(case["set_op"], kind, a, b, av, bv, desc)
@@ -86,6 +89,16 @@ def test_oracle_reproduces_reference_vectors(case):
     assert np.array_equal(_bits(keys_out), _bits(_keys(case, "expected_keys", kind)))
     if "expected_values" in case:
         assert vals_out.tolist() == case["expected_values"]
+
+
+def _arith(desc, kind):
+    """Items start + step * i of an arithmetic range, wrapping in the kind's width."""
+    start, step, n = desc
+    dt = np.dtype(NP[kind])
+    u = np.dtype(f"u{dt.itemsize}")
+    wrap = 1 << (8 * dt.itemsize)
+    vals = [(start + step * i) % wrap for i in range(n)]
+    return np.array(vals, dtype=np.uint64).astype(u).view(dt)
 
 
 # ---------------------------------------------------------------------------
