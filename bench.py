@@ -408,6 +408,71 @@ def run_record_sort(torch, np, abi, DeviceBuffer, wd, workloads, steps, warmup):
     return res
 
 
+def run_compaction(torch, np, abi, DeviceBuffer, workloads, steps, warmup):
+    """The reference's compaction and grouped-reduction benchmarks
+    (rccl-thrust/examples/compaction_benchmark.rs:62-109,
+    grouped_reduction_benchmark.rs:50-80): 2^20 + 13 u32 keys = index / 3;
+    unique_copy of the keys, and reduce_by_key with u64 values = index % 17 + 1
+    under NaturalBagAdd."""
+    n = workloads.RECORD_SORT_ROWS
+    launch_stream = torch.cuda.current_stream(0)
+    handle = launch_stream.cuda_stream
+    idx = torch.arange(n, dtype=torch.int64, device="cuda")
+    keys = _buffer(torch, DeviceBuffer, (idx // 3).to(torch.int32), np.uint32)
+    vals = _buffer(torch, DeviceBuffer, idx % 17 + 1, np.uint64)
+    out_k = DeviceBuffer.empty(np.uint32, n)
+    out_v = DeviceBuffer.empty(np.uint64, n)
+    count = DeviceBuffer.zeroed(np.uint64, 1)
+    lib = abi.load()
+    res = {}
+    groups = (n + 2) // 3
+    for name, op, pb_bytes in (("unique_copy", abi.GROUP_UNIQUE, 4.0 * n + 4.0 * groups),
+                               ("reduce_by_key", abi.GROUP_OPS["natural_bag_add"],
+                                12.0 * n + 12.0 * groups)):
+        ws_bytes = abi.workspace_bytes("rccl_hip_group_workspace_bytes", 0, 1, op, 0, n)
+        ws = DeviceBuffer.bytes(ws_bytes)
+
+        if name == "unique_copy":
+            def step(ws=ws, ws_bytes=ws_bytes):
+                abi.check(lib.rccl_hip_unique_copy(0, 1, 0, keys.ptr, None, out_k.ptr, None, n,
+                                                   count.ptr, ws.ptr, ws_bytes, handle))
+        else:
+            def step(ws=ws, ws_bytes=ws_bytes, op=op):
+                abi.check(lib.rccl_hip_reduce_by_key(0, 1, op, 0, keys.ptr, None, vals.ptr,
+                                                     out_k.ptr, None, out_v.ptr, n, count.ptr,
+                                                     ws.ptr, ws_bytes, handle))
+
+        ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, launch_stream, steps, warmup,
+                                                        step)
+        c = int(count.to_host_vec()[0])
+        ok = c == groups and bool(np.array_equal(out_k.to_host_vec()[:c],
+                                                 np.arange(groups, dtype=np.uint32)))
+        if name == "reduce_by_key":
+            v = (np.arange(n) % 17 + 1).astype(np.uint64)
+            expect = np.add.reduceat(v, np.arange(0, n, 3))
+            ok = ok and bool(np.array_equal(out_v.to_host_vec()[:c], expect))
+        res[name] = {
+            "value": round(n / (ms * 1e-3) / 1e9, 3), "unit": "Gitems/s",
+            "ms_per_step": round(ms, 4), "ms_per_step_min": round(ms_min, 4),
+            "roofline": roofline(pb_bytes, kms["group_tile"],
+                                 "group_tile (keys" + (" and values" if op else "") +
+                                 " read once, one output per run)"),
+            "kernel_ms": _rounded(kms), "validated": ok,
+        }
+    res["unique_copy"]["reference_published_ms"] = {
+        "rccl_sm89": 0.018739, "cub_sm89": 0.016790,
+        "source": "SRDATALOG_HISA_RCCL_TODO.md:178 (other hardware)"}
+    del keys, vals, out_k, out_v, count, idx
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"{n} u32 keys = index / 3 (runs of 3); reduce_by_key values u64 = "
+                    "index % 17 + 1, NaturalBagAdd",
+        "bytes_model": "unique_copy 4 B/key read + 4 B/run written; reduce_by_key 12 B/item "
+                       "read + 12 B/run written",
+        **res,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -515,8 +580,13 @@ def main():
         rsr = run_record_sort(torch, np, abi, DeviceBuffer, wd, workloads, args.steps,
                               args.warmup)
         _log(f"record sort: {rsr['ms_per_step']:.3f} ms")
-        out["ordering"] = {"merge": mg, "merge_sort": ms, "set_ops": so, "record_sort": rsr}
-        valid = valid and rsr["validated"]
+        _log("compaction")
+        cp = run_compaction(torch, np, abi, DeviceBuffer, workloads, args.steps, args.warmup)
+        _log("compaction done")
+        out["ordering"] = {"merge": mg, "merge_sort": ms, "set_ops": so, "record_sort": rsr,
+                           "compaction": cp}
+        valid = valid and rsr["validated"] and cp["unique_copy"]["validated"] and \
+            cp["reduce_by_key"]["validated"]
         valid = valid and mg["validated"] and ms["validated"] and all(
             so[op]["validated"] for op in ("union", "intersection", "difference",
                                            "symmetric_difference"))

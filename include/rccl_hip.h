@@ -88,6 +88,20 @@ typedef enum rccl_hip_set_operation {
   RCCL_HIP_SET_SYMMETRIC_DIFFERENCE = 3
 } rccl_hip_set_operation;
 
+/* Per-run operators of the adjacent-run compactions: UNIQUE keeps a run's
+ * first key; the others also fold the run's values left to right with the
+ * reference's sealed provenance operators
+ * (rccl-cub/src/grouped_reduction.rs:17-75): NATURAL_BAG_ADD on u64 (wrapping
+ * add), BOOLEAN_OR on one-byte BooleanProvenance (nonzero is true, the result
+ * is 0 or 1), INDEPENDENT_PROBABILITY_OR on f64 ((l + r) - l * r, each step
+ * rounded, clamped to [0, 1]). */
+typedef enum rccl_hip_group_op {
+  RCCL_HIP_GROUP_UNIQUE = 0,
+  RCCL_HIP_GROUP_NATURAL_BAG_ADD = 1,
+  RCCL_HIP_GROUP_BOOLEAN_OR = 2,
+  RCCL_HIP_GROUP_INDEPENDENT_PROBABILITY_OR = 3
+} rccl_hip_group_op;
+
 /* Details of the most recent failing call on this thread. `role` names the
  * offending range, as the reference's `role: &'static str` does. */
 typedef struct rccl_hip_error_info {
@@ -296,6 +310,50 @@ RCCL_HIP_API rccl_hip_status rccl_hip_set_op_arithmetic(
     rccl_hip_set_operation op, rccl_hip_key_kind key, rccl_hip_order order,
     const void *a_start, const void *a_step, size_t na, const void *b_start,
     const void *b_step, size_t nb, void *out_keys, size_t out_capacity, uint64_t *d_out_count,
+    void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Adjacent-run compaction (unique, reduce-by-key)
+ * ------------------------------------------------------------------------ */
+
+/* Keys are `key` scalars when arity == 1, or padding-free rows of `arity`
+ * (2..6) u32 columns when key == RCCL_HIP_KEY_U32. Adjacent keys are in one
+ * run when they compare equal (scalars with ==, so NaN keys never join a run;
+ * rows column by column). A key may carry a payload of payload_bytes per item
+ * (UNIQUE: 0, 1, 2, 4 or 8; the reductions: 0, 4 or 8) that takes no part in
+ * the comparison; each output gets the payload of its run's first item (the
+ * reference's key/value ranges compared by key). Workspace bytes for n keys. */
+RCCL_HIP_API rccl_hip_status rccl_hip_group_workspace_bytes(rccl_hip_key_kind key, uint32_t arity,
+                                                           rccl_hip_group_op op,
+                                                           size_t payload_bytes, size_t n,
+                                                           size_t *bytes);
+
+/* Stable adjacent unique: out_keys[0, count) (and out_payloads) = the first
+ * item of every run of in_keys[0, n); count is written to *d_count (device
+ * memory, one uint64_t). Outputs must hold n items and not overlap the
+ * inputs. Replaces unique_copy_by (rccl-thrust/src/compaction.rs:224-301)
+ * with the natural equivalence; the in-place unique_by (:303-378) is a copy
+ * to the scratch range followed by this call from the scratch back into the
+ * values. */
+RCCL_HIP_API rccl_hip_status rccl_hip_unique_copy(rccl_hip_key_kind key, uint32_t arity,
+                                                  size_t payload_bytes, const void *in_keys,
+                                                  const void *in_payloads, void *out_keys,
+                                                  void *out_payloads, size_t n, uint64_t *d_count,
+                                                  void *workspace, size_t workspace_bytes,
+                                                  hipStream_t stream);
+
+/* Reduce by key over sorted adjacent runs: for every run of equal adjacent
+ * keys, out_keys (and out_key_payloads) get its first item and out_values the
+ * left fold ((v0 op v1) op v2) ... of its values, in run order; the number of
+ * runs is written to *d_group_count. op is NATURAL_BAG_ADD (u64 values),
+ * BOOLEAN_OR (1-byte values) or INDEPENDENT_PROBABILITY_OR (f64 values).
+ * Outputs must hold n items and not overlap the inputs. Replaces
+ * reduce_by_key (rccl-thrust/src/grouped_reduction.rs:102-216,
+ * rccl-cub/src/grouped_reduction.rs:83-143) with the natural equivalence. */
+RCCL_HIP_API rccl_hip_status rccl_hip_reduce_by_key(
+    rccl_hip_key_kind key, uint32_t arity, rccl_hip_group_op op, size_t payload_bytes,
+    const void *keys, const void *key_payloads, const void *values, void *out_keys,
+    void *out_key_payloads, void *out_values, size_t n, uint64_t *d_group_count,
     void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus

@@ -70,6 +70,13 @@ def _load():
         lib.oracle_record_sort.restype = c.c_int
         lib.oracle_record_sort.argtypes = [c.c_uint, c.c_void_p, c.c_void_p, c.c_size_t,
                                            c.c_size_t]
+        lib.oracle_unique.restype = c.c_longlong
+        lib.oracle_unique.argtypes = [c.c_int, c.c_uint, c.c_void_p, c.c_void_p, c.c_size_t]
+        lib.oracle_reduce_by_key.restype = c.c_longlong
+        lib.oracle_reduce_by_key.argtypes = [c.c_int, c.c_uint, c.c_int, c.c_void_p, c.c_void_p,
+                                             c.c_void_p, c.c_void_p, c.c_size_t]
+        lib.oracle_prob_or.restype = c.c_double
+        lib.oracle_prob_or.argtypes = [c.c_double, c.c_double]
         lib.oracle_sort_unstable_u32.restype = c.c_int
         lib.oracle_sort_unstable_u32.argtypes = [c.c_void_p, c.c_size_t]
         lib.oracle_par_sort_unstable_u32.restype = c.c_int
@@ -193,3 +200,45 @@ def record_sort(rows, payloads=None):
     if _load().oracle_record_sort(r.shape[1], _ptr(r), _ptr(p), _vbytes(p), r.shape[0]) != 0:
         raise ValueError("oracle_record_sort: arity outside 2..6")
     return r, p
+
+
+GROUP_OPS = {"natural_bag_add": 1, "boolean_or": 2, "independent_probability_or": 3}
+GROUP_VALUE_DTYPES = {"natural_bag_add": np.uint64, "boolean_or": np.uint8,
+                      "independent_probability_or": np.float64}
+
+
+def _key_args(keys, kind):
+    """(kind code, arity, contiguous array) for scalar keys of `kind` or an
+    (n, arity) u32 row array (kind None)."""
+    if kind is None:
+        k = np.ascontiguousarray(keys, dtype=np.uint32)
+        return KEY_KINDS["u32"], k.shape[1], k
+    return KEY_KINDS[kind], 1, np.ascontiguousarray(keys)
+
+
+def unique(keys, kind=None):
+    """Stable adjacent unique of scalar keys (kind given) or rows (kind None)."""
+    code, arity, k = _key_args(keys, kind)
+    out = np.empty_like(k)
+    n = _load().oracle_unique(code, arity, _ptr(k), _ptr(out), len(k))
+    if n < 0:
+        raise ValueError("oracle_unique: invalid key")
+    return out[:n]
+
+
+def reduce_by_key(keys, values, op, kind=None):
+    """(run keys, run aggregates) of adjacent equal keys; op is one of
+    GROUP_OPS."""
+    code, arity, k = _key_args(keys, kind)
+    v = np.ascontiguousarray(values, dtype=GROUP_VALUE_DTYPES[op])
+    out_k = np.empty_like(k)
+    out_v = np.empty_like(v)
+    n = _load().oracle_reduce_by_key(code, arity, GROUP_OPS[op], _ptr(k), _ptr(v), _ptr(out_k),
+                                     _ptr(out_v), len(k))
+    if n < 0:
+        raise ValueError("oracle_reduce_by_key: invalid key or operator")
+    return out_k[:n], out_v[:n]
+
+
+def prob_or(l: float, r: float) -> float:
+    return _load().oracle_prob_or(l, r)

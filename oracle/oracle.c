@@ -338,3 +338,97 @@ long long oracle_set_op(int op, int kind, int descending, const void *a_keys,
 #undef EMIT
   return o;
 }
+
+/* Adjacent-run compactions: rccl-cub/src/compaction_kernels.rs:64-93 (an item
+ * starts a run when it is first or not equivalent to its predecessor),
+ * :95-131 (stable scatter of the heads) and :180-236 (one left fold per run,
+ * in index order), with the natural equivalence: == on the key's value
+ * (floats by IEEE ==), every column for rows. */
+static int key_equal(int kind, unsigned arity, const void *keys, size_t i, size_t j) {
+  if (arity > 1) {
+    const uint32_t *r = (const uint32_t *)keys;
+    for (unsigned c = 0; c < arity; ++c)
+      if (r[i * arity + c] != r[j * arity + c]) return 0;
+    return 1;
+  }
+  switch (kind) {
+  case ORACLE_KEY_F32: return ((const float *)keys)[i] == ((const float *)keys)[j];
+  case ORACLE_KEY_F64: return ((const double *)keys)[i] == ((const double *)keys)[j];
+  default: {
+    const int kb = kind_bytes(kind);
+    return memcmp((const char *)keys + i * kb, (const char *)keys + j * kb, (size_t)kb) == 0;
+  }
+  }
+}
+
+static size_t key_width(int kind, unsigned arity) {
+  return arity > 1 ? (size_t)arity * 4u : (size_t)kind_bytes(kind);
+}
+
+static int valid_key(int kind, unsigned arity) {
+  if (arity == 1) return kind_bytes(kind) > 0;
+  return kind == ORACLE_KEY_U32 && arity >= 2 && arity <= 6;
+}
+
+long long oracle_unique(int kind, unsigned arity, const void *in, void *out, size_t n) {
+  if (!valid_key(kind, arity)) return -1;
+  const size_t kb = key_width(kind, arity);
+  size_t count = 0;
+  for (size_t i = 0; i < n; ++i) {
+    if (i == 0 || !key_equal(kind, arity, in, i - 1, i)) {
+      memcpy((char *)out + count * kb, (const char *)in + i * kb, kb);
+      ++count;
+    }
+  }
+  return (long long)count;
+}
+
+/* The sealed operators of rccl-cub/src/grouped_reduction.rs:17-75. */
+static uint64_t bag_add(uint64_t l, uint64_t r) { return l + r; }
+static uint8_t bool_or(uint8_t l, uint8_t r) { return (l != 0 || r != 0) ? 1 : 0; }
+static double prob_or(double l, double r) {
+  /* (l + r) - (l * r), each step rounded (built with -ffp-contract=off). */
+  volatile double s = l + r;
+  volatile double p = l * r;
+  double c = s - p;
+  if (c < 0.0) return 0.0;
+  if (c > 1.0) return 1.0;
+  return c;
+}
+
+long long oracle_reduce_by_key(int kind, unsigned arity, int op, const void *keys,
+                               const void *values, void *out_keys, void *out_values, size_t n) {
+  if (!valid_key(kind, arity) || op < ORACLE_GROUP_NATURAL_BAG_ADD ||
+      op > ORACLE_GROUP_INDEPENDENT_PROBABILITY_OR)
+    return -1;
+  const size_t kb = key_width(kind, arity);
+  size_t count = 0;
+  size_t i = 0;
+  while (i < n) {
+    size_t j = i + 1;
+    while (j < n && key_equal(kind, arity, keys, j - 1, j)) ++j;
+    memcpy((char *)out_keys + count * kb, (const char *)keys + i * kb, kb);
+    if (op == ORACLE_GROUP_NATURAL_BAG_ADD) {
+      const uint64_t *v = (const uint64_t *)values;
+      uint64_t agg = v[i];
+      for (size_t k = i + 1; k < j; ++k) agg = bag_add(agg, v[k]);
+      ((uint64_t *)out_values)[count] = agg;
+    } else if (op == ORACLE_GROUP_BOOLEAN_OR) {
+      const uint8_t *v = (const uint8_t *)values;
+      uint8_t agg = v[i];
+      for (size_t k = i + 1; k < j; ++k) agg = bool_or(agg, v[k]);
+      ((uint8_t *)out_values)[count] = agg;
+    } else {
+      const double *v = (const double *)values;
+      double agg = v[i];
+      for (size_t k = i + 1; k < j; ++k) agg = prob_or(agg, v[k]);
+      ((double *)out_values)[count] = agg;
+    }
+    ++count;
+    i = j;
+  }
+  return (long long)count;
+}
+
+/* One operator step, for the known-answer tests. */
+double oracle_prob_or(double l, double r) { return prob_or(l, r); }

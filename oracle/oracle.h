@@ -18,6 +18,12 @@
  *   oracle_merge_sort   reference literal vectors, Python sorted() (stable).
  *   oracle_set_op       reference literal vectors (incl. by-key value
  *                       selection), collections.Counter multiset algebra.
+ *   oracle_record_sort  reference literal vectors, numpy's stable lexsort.
+ *   oracle_unique,
+ *   oracle_reduce_by_key reference literal vectors (examples/compaction.rs,
+ *                       examples/grouped_reduction.rs), the reference's
+ *                       operator known answers (grouped_reduction.rs:209-224),
+ *                       an itertools.groupby restatement in the tests.
  *   oracle_splitmix64   published splitmix64 test value.
  */
 #ifndef RCCL_ORACLE_H
@@ -87,6 +93,26 @@ long long oracle_set_op(int op, int kind, int descending, const void *a_keys,
  * Returns 0, or -1 for an arity outside 2..6. */
 int oracle_record_sort(unsigned arity, uint32_t *rows, void *payloads,
                        size_t payload_bytes, size_t n);
+
+/* Reduce-by-key operators; numbering equals rccl_hip_group_op. */
+enum {
+  ORACLE_GROUP_NATURAL_BAG_ADD = 1,
+  ORACLE_GROUP_BOOLEAN_OR = 2,
+  ORACLE_GROUP_INDEPENDENT_PROBABILITY_OR = 3
+};
+
+/* Stable adjacent unique of n keys (`kind` scalars when arity == 1, rows of
+ * `arity` u32 columns otherwise). Returns the number of runs, or -1. */
+long long oracle_unique(int kind, unsigned arity, const void *in, void *out, size_t n);
+
+/* Reduce by key: first key and left fold of the values of every run of equal
+ * adjacent keys. Values are u64 (NATURAL_BAG_ADD), u8 (BOOLEAN_OR) or f64
+ * (INDEPENDENT_PROBABILITY_OR). Returns the number of runs, or -1. */
+long long oracle_reduce_by_key(int kind, unsigned arity, int op, const void *keys,
+                               const void *values, void *out_keys, void *out_values, size_t n);
+
+/* One INDEPENDENT_PROBABILITY_OR step. */
+double oracle_prob_or(double l, double r);
 
 #ifdef __cplusplus
 }

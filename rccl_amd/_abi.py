@@ -37,6 +37,8 @@ RADIX_KINDS = ("u32", "i32", "f32", "u64", "i64", "f64")
 ASCENDING = 0
 DESCENDING = 1
 SET_OPS = {"union": 0, "intersection": 1, "difference": 2, "symmetric_difference": 3}
+GROUP_UNIQUE = 0
+GROUP_OPS = {"natural_bag_add": 1, "boolean_or": 2, "independent_probability_or": 3}
 
 # The exported C symbols; a test checks the library exports each one.
 EXPORTED_SYMBOLS = (
@@ -58,6 +60,9 @@ EXPORTED_SYMBOLS = (
     "rccl_hip_set_op_arithmetic",
     "rccl_hip_record_sort_workspace_bytes",
     "rccl_hip_record_sort",
+    "rccl_hip_group_workspace_bytes",
+    "rccl_hip_unique_copy",
+    "rccl_hip_reduce_by_key",
 )
 
 
@@ -165,6 +170,15 @@ def _declare(lib):
     lib_view.rccl_hip_set_op.restype = st
     lib_view.rccl_hip_set_op.argtypes = [st, st, sz, st, vp, vp, sz, vp, vp, sz, vp, vp, sz, vp, vp,
                                          sz, vp]
+    lib_view.rccl_hip_group_workspace_bytes.restype = st
+    lib_view.rccl_hip_group_workspace_bytes.argtypes = [st, c.c_uint32, st, sz, sz,
+                                                        c.POINTER(sz)]
+    lib_view.rccl_hip_unique_copy.restype = st
+    lib_view.rccl_hip_unique_copy.argtypes = [st, c.c_uint32, sz, vp, vp, vp, vp, sz, vp, vp, sz,
+                                              vp]
+    lib_view.rccl_hip_reduce_by_key.restype = st
+    lib_view.rccl_hip_reduce_by_key.argtypes = [st, c.c_uint32, st, sz, vp, vp, vp, vp, vp, vp,
+                                                sz, vp, vp, sz, vp]
     lib_view.rccl_hip_set_op_arithmetic.restype = st
     lib_view.rccl_hip_set_op_arithmetic.argtypes = [st, st, st, vp, vp, sz, vp, vp, sz, vp, sz, vp,
                                                     vp, sz, vp]

@@ -1,0 +1,9 @@
+// Adjacent-run compaction instantiation for i32 keys (unique and the three
+// reduce-by-key operators).
+#include "group_kernels.hpp"
+
+namespace rccl_hip {
+namespace group {
+RCCL_GROUP_DEFINE_KEY(i32, int32_t)
+} // namespace group
+} // namespace rccl_hip

@@ -1,0 +1,9 @@
+// Adjacent-run compaction instantiation for i8 keys (unique and the three
+// reduce-by-key operators).
+#include "group_kernels.hpp"
+
+namespace rccl_hip {
+namespace group {
+RCCL_GROUP_DEFINE_KEY(i8, int8_t)
+} // namespace group
+} // namespace rccl_hip

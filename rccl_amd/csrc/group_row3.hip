@@ -1,0 +1,9 @@
+// Adjacent-run compaction instantiation for row3 keys (unique and the three
+// reduce-by-key operators).
+#include "group_kernels.hpp"
+
+namespace rccl_hip {
+namespace group {
+RCCL_GROUP_DEFINE_KEY(row3, record_sort::Row<3>)
+} // namespace group
+} // namespace rccl_hip

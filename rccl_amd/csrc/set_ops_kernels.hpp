@@ -11,14 +11,16 @@
 //              path per thread in LDS, ITEMS steps of the serial operation,
 //              a block scan of the emitted counts, a two-level decoupled
 //              look-back for the tile's global output offset (a whole wave
-//              polls 64 predecessors at once), LDS-compacted coalesced
-//              stores; the last tile writes the output count
+//              polls 64 predecessors at once, tile_lookback.hpp),
+//              LDS-compacted coalesced stores; the last tile writes the
+//              output count
 #pragma once
 
 #include <algorithm>
 #include <cstring>
 
 #include "ordering_common.hpp"
+#include "tile_lookback.hpp"
 
 namespace rccl_hip {
 namespace set_ops {
@@ -27,7 +29,7 @@ using ordering::NoValue;
 
 constexpr int THREADS = 512;
 constexpr int WAVES = THREADS / 64;
-constexpr int GROUP = 64;  // tiles per look-back group (one wave polls a group)
+constexpr size_t GROUP = lookback::GROUP;
 
 enum Op : int { UNION = 0, INTERSECTION = 1, DIFFERENCE = 2, SYMMETRIC_DIFFERENCE = 3 };
 
@@ -40,12 +42,6 @@ template <class K, class V>
 constexpr size_t tile_items() {
   return size_t(THREADS) * items_for<K, V>();
 }
-
-// Look-back words: 2 flag bits over a 62-bit count.
-constexpr uint64_t F_AGG = 1ull << 62, F_INCL = 2ull << 62, VMASK = (1ull << 62) - 1;
-// Group aggregate: tiles counted in the top 16 bits, count below.
-constexpr int GA_SHIFT = 48;
-constexpr uint64_t GA_MASK = (1ull << GA_SHIFT) - 1;
 
 // Finite arithmetic input range: item i is start + step * i in the key's own
 // wrapping integer arithmetic (rccl-cub/src/ordering_backend/set.rs:49-81,
@@ -145,12 +141,6 @@ __global__ void __launch_bounds__(256) clear_kernel(uint64_t *p, size_t words) {
     p[i] = 0;
 }
 } // namespace
-
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
 
 template <class K, class V, int ITEMS>
 struct TileSmem {
@@ -329,64 +319,9 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
 
   // Two-level decoupled look-back for the tile's output offset (wave 0).
   if (wave == 0) {
-    const size_t g = t / GROUP;
-    const size_t gfirst = g * GROUP;
-    const uint32_t pos = static_cast<uint32_t>(t - gfirst);
+    const uint64_t prefix =
+        lookback::tile_prefix(t, tiles, tile_count, desc, gagg, ginc, lane);
     if (lane == 0) {
-      store_agent(&desc[t], (t == 0 ? F_INCL : F_AGG) | uint64_t(tile_count));
-      add_agent(&gagg[g], uint64_t((1ull << GA_SHIFT) | tile_count));
-    }
-    uint64_t prefix = 0;
-    if (t > 0) {
-      bool done = false;
-      if (pos > 0) {
-        // In-group predecessors: lane l polls tile gfirst + l (l < pos) until
-        // every one has published; the sum then runs from the newest
-        // inclusive prefix (if any) up to this tile.
-        uint64_t d;
-        while (true) {
-          d = lane < pos ? load_agent(&desc[gfirst + lane]) : F_AGG;
-          if (__ballot((d >> 62) == 0) == 0) break;
-          __builtin_amdgcn_s_sleep(1);
-        }
-        const uint64_t incl = __ballot(lane < pos && (d >> 62) == 2);
-        const int hi = incl ? 63 - __clzll(static_cast<long long>(incl)) : -1;
-        prefix = wave_sum_u64((lane < pos && int(lane) >= hi) ? (d & VMASK) : 0);
-        done = hi >= 0;
-      }
-      // Earlier groups, newest first, 64 at a time: complete aggregates are
-      // summed until a group's inclusive prefix (groups before the first are
-      // read as an inclusive zero).
-      long long gg = static_cast<long long>(g) - 1;
-      while (!done) {
-        const long long gi = gg - static_cast<long long>(lane);
-        const uint64_t inc_w = gi >= 0 ? load_agent(&ginc[gi]) : F_INCL;
-        const uint64_t agg_w = gi >= 0 ? load_agent(&gagg[gi]) : 0;
-        const uint64_t incl_lanes = __ballot((inc_w >> 62) == 2);
-        const uint64_t full_lanes = __ballot((agg_w >> GA_SHIFT) == uint64_t(GROUP));
-        // First lane (newest group) holding an inclusive prefix, if any.
-        const int first_incl = incl_lanes ? __ffsll(static_cast<long long>(incl_lanes)) - 1 : 64;
-        // Groups before it must all be complete to be summed.
-        const uint64_t before = first_incl == 64 ? ~0ull : ((1ull << first_incl) - 1);
-        const int first_gap = (~full_lanes & before) ? __ffsll(static_cast<long long>(~full_lanes & before)) - 1 : 64;
-        if (first_gap < first_incl) {
-          // Sum the complete groups before the gap and poll again from it.
-          prefix += wave_sum_u64(int(lane) < first_gap ? (agg_w & GA_MASK) : 0);
-          gg -= first_gap;
-          if (first_gap == 0) __builtin_amdgcn_s_sleep(1);
-          continue;
-        }
-        uint64_t v = int(lane) < first_incl ? (agg_w & GA_MASK) : 0;
-        if (int(lane) == first_incl) v = inc_w & VMASK;
-        prefix += wave_sum_u64(v);
-        if (first_incl < 64) break;
-        gg -= 64;
-      }
-      if (lane == 0) store_agent(&desc[t], F_INCL | (prefix + tile_count));
-    }
-    const size_t glast = std::min(gfirst + GROUP, tiles) - 1;
-    if (lane == 0) {
-      if (t == glast) store_agent(&ginc[g], F_INCL | (prefix + tile_count));
       if (t + 1 == tiles && out_count) *out_count = prefix + tile_count;
       sm.tile_offset = prefix;
     }

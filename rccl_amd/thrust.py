@@ -10,17 +10,21 @@ StarGazerM/rccl tree):
   arithmetic_range(..).difference(..)  set.rs:127-244,477-690 (unmaterialised inputs)
   a.union(b).write_into / .count       set.rs:357-898 (also intersection,
                                        difference, symmetric_difference)
+  unique_copy_by, unique_by            compaction.rs:224-378
+  reduce_by_key + NaturalBagAdd,       grouped_reduction.rs:102-216
+    BooleanOr, IndependentProbabilityOr
 Every call allocates its temporary workspace on the device, runs on the
 execution's stream and synchronizes before returning, as Thrust's
 synchronous policy does (rccl-thrust/src/backend.rs:8-150).
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
-from . import cub
+from . import _abi, cub
 from ._abi import DeviceAlgorithmError  # noqa: F401  (re-export)
-from .device import DeviceBuffer
+from .device import DeviceBuffer, kind_of
 
 ascending = cub.ascending
 descending = cub.descending
@@ -318,3 +322,146 @@ class _SetExpression:
     def count(self, execution: Execution) -> int:
         """Execute the operation without materializing its keys."""
         return self._run(None, execution)
+
+
+# ---------------------------------------------------------------------------
+# Adjacent-run compaction (rccl-thrust/src/compaction.rs:224-378,
+# grouped_reduction.rs:102-216).
+# ---------------------------------------------------------------------------
+# The natural equivalence, |a, b| a == b (on keys; key/value ranges compare by
+# key). Other closures have no kernels.
+equal = "equal"
+
+
+class NaturalBagAdd:
+    """u64 wrapping addition (rccl-cub/src/grouped_reduction.rs:22-31)."""
+    code, dtype = _abi.GROUP_OPS["natural_bag_add"], np.dtype(np.uint64)
+
+
+class BooleanOr:
+    """BooleanProvenance (one byte) disjunction (grouped_reduction.rs:49-57)."""
+    code, dtype = _abi.GROUP_OPS["boolean_or"], np.dtype(np.uint8)
+
+
+class IndependentProbabilityOr:
+    """f64 l + r - l * r, clamped to [0, 1] (grouped_reduction.rs:59-75)."""
+    code, dtype = _abi.GROUP_OPS["independent_probability_or"], np.dtype(np.float64)
+
+
+def _check_equivalent(equivalent):
+    if equivalent is not equal and equivalent is not None:
+        raise ValueError("only the natural equivalence (thrust.equal) has device kernels")
+
+
+def _group_keys(rng):
+    """(key kind code, arity, keys buffer, payload buffer | None) of a key
+    range: a DeviceBuffer / view of scalars, a RowBuffer of rows, or a
+    key/value range (keys compared, values carried as the key's payload)."""
+    from .record_sort import RowBuffer
+
+    payload = None
+    if isinstance(rng, KeyValueRange):
+        payload = rng.values.buffer
+        rng = rng.keys
+    elif isinstance(rng, tuple):
+        rng, payload = rng
+        payload = payload.buffer if isinstance(payload, DeviceView) else payload
+    if isinstance(rng, DeviceView):
+        rng = rng.buffer
+    if isinstance(rng, RowBuffer):
+        return _abi.KEY_KINDS["u32"], rng.arity, rng, payload
+    return _abi.KEY_KINDS[kind_of(rng.dtype)], 1, rng, payload
+
+
+def _capacity(role, needed, actual):
+    if actual < needed:
+        info = _abi.ErrorInfo()
+        info.status, info.role, info.expected, info.actual = 2, role.encode(), needed, actual
+        raise DeviceAlgorithmError(2, info)
+
+
+def _count_buffer(count, role):
+    _capacity(role, 1, count.len())
+
+
+def _group_workspace(execution, kind, arity, op, pb, n):
+    nbytes = _abi.workspace_bytes("rccl_hip_group_workspace_bytes", kind, arity, op, pb, n)
+    return DeviceBuffer.bytes(nbytes, execution.launch().program.device), nbytes
+
+
+def _unique(execution, kind, arity, keys, pay, out_keys, out_pay, n, count):
+    pb = 0 if pay is None else pay.dtype.itemsize
+    ws, nbytes = _group_workspace(execution, kind, arity, _abi.GROUP_UNIQUE, pb, n)
+    _abi.check(_abi.load().rccl_hip_unique_copy(
+        kind, arity, pb, keys.ptr, None if pay is None else pay.ptr, out_keys.ptr,
+        None if out_pay is None else out_pay.ptr, n, count.ptr, ws.ptr, nbytes,
+        execution.launch().handle))
+
+
+def unique_copy_by(execution, input, output, selected_count, equivalent=equal):
+    """Stably copy the first item of every run of equivalent adjacent items
+    into output's prefix; the number kept lands in selected_count[0]."""
+    _check_equivalent(equivalent)
+    kind, arity, keys, pay = _group_keys(input)
+    _, o_arity, out_keys, out_pay = _group_keys(output)
+    n = keys.len()
+    _capacity("unique-copy output", n, out_keys.len())
+    if (pay is None) != (out_pay is None):
+        raise TypeError("input and output must both carry values or neither")
+    if pay is not None:
+        _capacity("unique-copy output", n, out_pay.len())
+    _count_buffer(selected_count, "selected-count output")
+    _unique(execution, kind, arity, keys, pay, out_keys, out_pay, n, selected_count)
+    execution.synchronize()
+
+
+def unique_by(execution, values, scratch, selected_count, equivalent=equal):
+    """In-place adjacent unique: values' prefix holds the first item of every
+    run, the rest of values is left as it was; scratch (same length) is
+    overwritten."""
+    _check_equivalent(equivalent)
+    kind, arity, keys, pay = _group_keys(values)
+    _, _, s_keys, s_pay = _group_keys(scratch)
+    n = keys.len()
+    _capacity("unique scratch", n, s_keys.len())
+    if s_keys.len() != n:
+        cub._check_len("unique scratch", n, s_keys.len())
+    _count_buffer(selected_count, "selected-count output")
+    # The values are copied to the scratch on the execution's stream, then
+    # compacted from the scratch back into the values.
+    with torch.cuda.stream(execution.launch().stream()):
+        if arity > 1:
+            s_keys.words.tensor.copy_(keys.words.tensor)
+        else:
+            s_keys.tensor.copy_(keys.tensor)
+        if pay is not None:
+            s_pay.tensor.copy_(pay.tensor)
+    _unique(execution, kind, arity, s_keys, s_pay, keys, pay, n, selected_count)
+    execution.synchronize()
+
+
+def reduce_by_key(execution, keys, values, output_keys, output_values, group_count,
+                  equivalent=equal, operator=NaturalBagAdd):
+    """For every run of equivalent adjacent keys: its first key (and key
+    payload) and the left fold of its values with `operator`; the number of
+    runs lands in group_count[0]."""
+    _check_equivalent(equivalent)
+    kind, arity, k, kp = _group_keys(keys)
+    _, _, ok, okp = _group_keys(output_keys)
+    vals = values.buffer if isinstance(values, DeviceView) else values
+    outv = output_values.buffer if isinstance(output_values, DeviceView) else output_values
+    n = k.len()
+    if vals.len() != n:
+        cub._check_len("reduce-by-key values", n, vals.len())
+    _capacity("reduce-by-key key output", n, ok.len())
+    _capacity("reduce-by-key aggregate output", n, outv.len())
+    _count_buffer(group_count, "group-count output")
+    if vals.dtype != operator.dtype or outv.dtype != operator.dtype:
+        raise TypeError(f"{operator.__name__} reduces {operator.dtype} values")
+    pb = 0 if kp is None else kp.dtype.itemsize
+    ws, nbytes = _group_workspace(execution, kind, arity, operator.code, pb, n)
+    _abi.check(_abi.load().rccl_hip_reduce_by_key(
+        kind, arity, operator.code, pb, k.ptr, None if kp is None else kp.ptr, vals.ptr, ok.ptr,
+        None if okp is None else okp.ptr, outv.ptr, n, group_count.ptr, ws.ptr, nbytes,
+        execution.launch().handle))
+    execution.synchronize()

@@ -149,6 +149,30 @@ def test_arithmetic_range_host_items():
         cub.arithmetic_range(np.float32(0), np.float32(1), 3)
 
 
+def test_group_validation(lib):
+    out = ctypes.c_size_t()
+    # Keys: scalar kinds at arity 1, u32 rows at arity 2..6.
+    assert lib.rccl_hip_group_workspace_bytes(0, 1, 0, 0, 100, ctypes.byref(out)) == 0
+    assert lib.rccl_hip_group_workspace_bytes(0, 6, 0, 0, 100, ctypes.byref(out)) == 0
+    assert lib.rccl_hip_group_workspace_bytes(0, 7, 0, 0, 100, ctypes.byref(out)) == 9
+    assert lib.rccl_hip_group_workspace_bytes(3, 2, 0, 0, 100, ctypes.byref(out)) == 9  # u64 rows
+    assert lib.rccl_hip_group_workspace_bytes(0, 1, 4, 0, 100, ctypes.byref(out)) == 9  # operator
+    # Payload widths: unique 0/1/2/4/8, reductions 0/4/8.
+    assert lib.rccl_hip_group_workspace_bytes(0, 1, 0, 2, 100, ctypes.byref(out)) == 0
+    assert lib.rccl_hip_group_workspace_bytes(0, 1, 1, 2, 100, ctypes.byref(out)) == 9
+    assert lib.rccl_hip_group_workspace_bytes(0, 1, 0, 16, 100, ctypes.byref(out)) == 9
+    need = _abi.workspace_bytes("rccl_hip_group_workspace_bytes", 0, 1, 1, 0, 1 << 20)
+    assert 0 < need < (1 << 20)  # look-back state only
+    assert lib.rccl_hip_reduce_by_key(0, 1, 1, 0, FAKE, None, FAKE, FAKE, None, FAKE, 1 << 20,
+                                      FAKE, FAKE, need - 1, None) == 2
+    assert lib.rccl_hip_reduce_by_key(0, 1, 0, 0, FAKE, None, FAKE, FAKE, None, FAKE, 10, FAKE,
+                                      FAKE, need, None) == 9  # UNIQUE is not a reduction
+    assert lib.rccl_hip_reduce_by_key(0, 1, 1, 0, FAKE, None, FAKE, FAKE, None, FAKE, 10, None,
+                                      FAKE, need, None) == 9  # count required
+    assert lib.rccl_hip_unique_copy(0, 1, 8, FAKE, None, FAKE, FAKE, 10, FAKE, FAKE, need,
+                                    None) == 9  # payload pointers required
+
+
 def test_record_sort_validation(lib):
     out = ctypes.c_size_t()
     # Arity 2..6 only (rccl-thrust/src/record_sort.rs:117-126).

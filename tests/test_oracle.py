@@ -57,6 +57,9 @@ def test_oracle_reproduces_reference_vectors(case):
         if "expected_payloads" in case:
             assert out_pay.tolist() == case["expected_payloads"]
         return
+    if case["op"] in ("unique", "reduce_by_key"):
+        _check_group_case(case)
+        return
     kind, desc = case["kind"], case["descending"]
     vdt = NP.get(case.get("value_dtype", ""), None)
     if case["op"] == "radix_sort":
@@ -89,6 +92,48 @@ def test_oracle_reproduces_reference_vectors(case):
     assert np.array_equal(_bits(keys_out), _bits(_keys(case, "expected_keys", kind)))
     if "expected_values" in case:
         assert vals_out.tolist() == case["expected_values"]
+
+
+def _group_case_arrays(case):
+    """Keys, payloads, values and expected outputs of a unique/reduce golden case."""
+    keys = np.array(case["keys"], dtype=NP[case["kind"]])
+    pays = None
+    if "payloads" in case:
+        pays = np.array(case["payloads"], dtype=NP[case["payload_dtype"]])
+    vals = None
+    if "values" in case:
+        vals = np.array(case["values"], dtype=oracle.GROUP_VALUE_DTYPES[case["group_op"]])
+    elif "values_f64_bits" in case:
+        vals = np.array(case["values_f64_bits"], dtype=np.uint64).view(np.float64)
+    if "expected_values_f64_bits" in case:
+        exp_vals = np.array(case["expected_values_f64_bits"], dtype=np.uint64)
+    elif "expected_values" in case:
+        exp_vals = np.array(case["expected_values"], dtype=np.uint64)
+    else:
+        exp_vals = None
+    return keys, pays, vals, exp_vals
+
+
+def _run_lengths_first(keys):
+    """Indices of run heads (first of each run of equal adjacent keys)."""
+    return [i for i in range(len(keys)) if i == 0 or keys[i - 1] != keys[i]]
+
+
+def _check_group_case(case):
+    keys, pays, vals, exp_vals = _group_case_arrays(case)
+    heads = _run_lengths_first(keys)
+    if case["op"] == "unique":
+        out = oracle.unique(keys, case["kind"])
+        assert out.tolist() == case["expected_keys"]
+        # The payload of a run is its first item's.
+        assert pays[heads].tolist() == case["expected_payloads"]
+        return
+    out_k, out_v = oracle.reduce_by_key(keys, vals, case["group_op"], case["kind"])
+    assert out_k.tolist() == case["expected_keys"]
+    assert np.array_equal(out_v.view(np.uint64) if out_v.dtype == np.float64 else
+                          out_v.astype(np.uint64), exp_vals)
+    if pays is not None:
+        assert pays[heads].tolist() == case["expected_payloads"]
 
 
 def _arith(desc, kind):
@@ -367,3 +412,76 @@ def test_record_sort_oracle_rejects_arity():
         oracle.record_sort(np.zeros((3, 1), dtype=np.uint32))
     with pytest.raises(ValueError):
         oracle.record_sort(np.zeros((3, 7), dtype=np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# Adjacent-run compactions vs an itertools.groupby restatement
+# (rccl-cub/src/compaction_kernels.rs:64-236, grouped_reduction.rs:17-75).
+# ---------------------------------------------------------------------------
+def _groupby_reduce(keys, vals, op):
+    import itertools
+    out_k, out_v = [], []
+    idx = 0
+    for key, grp in itertools.groupby(keys.tolist() if keys.ndim == 1 else
+                                      [tuple(r) for r in keys.tolist()]):
+        n = len(list(grp))
+        run = vals[idx:idx + n].tolist()
+        idx += n
+        if op == "natural_bag_add":
+            agg = run[0]
+            for v in run[1:]:
+                agg = (agg + v) % (1 << 64)
+        elif op == "boolean_or":
+            agg = run[0]
+            for v in run[1:]:
+                agg = 1 if (agg or v) else 0
+        else:
+            agg = run[0]
+            for v in run[1:]:
+                agg = min(max(agg + v - agg * v, 0.0), 1.0)
+        out_k.append(key)
+        out_v.append(agg)
+    return out_k, out_v
+
+
+@pytest.mark.parametrize("op", ["natural_bag_add", "boolean_or", "independent_probability_or"])
+def test_reduce_by_key_oracle_vs_groupby(op):
+    rng = np.random.default_rng(11)
+    for n in (0, 1, 2, 31, 257, 5000):
+        keys = np.sort(rng.integers(0, max(1, n // 4), size=n)).astype(np.int32)
+        vals = {"natural_bag_add": rng.integers(0, 2**64, size=n, dtype=np.uint64),
+                "boolean_or": rng.integers(0, 2, size=n).astype(np.uint8),
+                "independent_probability_or": rng.random(n)}[op]
+        exp_k, exp_v = _groupby_reduce(keys, vals, op)
+        out_k, out_v = oracle.reduce_by_key(keys, vals, op, "i32")
+        assert out_k.tolist() == exp_k
+        assert out_v.tolist() == exp_v  # Python floats fold without fused multiply-add
+    # Rows: a run is a run of equal rows.
+    rows = np.repeat(rng.integers(0, 3, size=(400, 3)).astype(np.uint32), 3, axis=0)
+    vals = rng.integers(0, 100, size=len(rows), dtype=np.uint64)
+    exp_k, exp_v = _groupby_reduce(rows, vals, "natural_bag_add")
+    out_k, out_v = oracle.reduce_by_key(rows, vals, "natural_bag_add")
+    assert [tuple(r) for r in out_k.tolist()] == exp_k and out_v.tolist() == exp_v
+
+
+def test_unique_oracle_vs_groupby():
+    import itertools
+    rng = np.random.default_rng(12)
+    for n in (0, 1, 31, 32, 33, 255, 256, 257, 513):
+        keys = (np.arange(n) // 3).astype(np.uint32)  # examples/compaction.rs:117-146
+        assert oracle.unique(keys, "u32").tolist() == [k for k, _ in itertools.groupby(keys)]
+    f = np.array([0.0, -0.0, np.nan, np.nan, 1.0, 1.0], dtype=np.float64)
+    # IEEE ==: -0 joins the run of +0, NaN never joins a run.
+    assert oracle.unique(f, "f64").view(np.uint64).tolist() == \
+        f[[0, 2, 3, 4]].view(np.uint64).tolist()
+    rows = rng.integers(0, 2, size=(1000, 2)).astype(np.uint32)
+    exp = [k for k, _ in itertools.groupby([tuple(r) for r in rows.tolist()])]
+    assert [tuple(r) for r in oracle.unique(rows).tolist()] == exp
+
+
+def test_probability_or_known_answers():
+    """rccl-cub/src/grouped_reduction.rs:209-224."""
+    import struct
+    second = oracle.prob_or(oracle.prob_or(0.1, 0.2), 0.3)
+    assert struct.unpack("<Q", struct.pack("<d", second))[0] == 4_602_606_761_578_608_985
+    assert oracle.prob_or(1.0, 0.5) == 1.0
