@@ -473,6 +473,41 @@ def run_compaction(torch, np, abi, DeviceBuffer, workloads, steps, warmup):
     }
 
 
+def run_search(torch, np, abi, DeviceBuffer, wd, log2_hay, log2_q, steps, warmup):
+    """Vectorized lower_bound: 2^log2_hay sorted u32 keys in [0, 2^24) (the C4
+    merge sort keys, sorted), 2^log2_q needles from the same distribution."""
+    n, m = 1 << log2_hay, 1 << log2_q
+    hay_t = torch.sort(wd.c4_merge_sort_keys(n).to(torch.int64)).values.to(torch.int32)
+    q_t = wd.c4_merge_sort_keys(m)
+    hay = _buffer(torch, DeviceBuffer, hay_t, np.uint32)
+    q = _buffer(torch, DeviceBuffer, q_t, np.uint32)
+    out = DeviceBuffer.empty(np.uint64, m)
+    stream = torch.cuda.current_stream(0)
+    lib = abi.load()
+
+    def step():
+        abi.check(lib.rccl_hip_bound_search(0, 1, 0, 0, hay.ptr, n, q.ptr, m, out.ptr,
+                                            stream.cuda_stream))
+
+    ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, stream, steps, warmup, step)
+    # Validate against torch.searchsorted on the device (same definition).
+    expect = torch.searchsorted(hay_t.to(torch.int64), q_t.to(torch.int64), right=False)
+    ok = bool(torch.equal(out.tensor[:m], expect))
+    res = {
+        "workload": f"lower_bound of 2^{log2_q} u32 needles in a sorted 2^{log2_hay} u32 "
+                    "haystack (values in [0, 2^24))",
+        "value": round(m / (ms * 1e-3) / 1e9, 3), "unit": "Gqueries/s",
+        "ms_per_step": round(ms, 4), "ms_per_step_min": round(ms_min, 4),
+        "bytes_model": "12 B/query (needle read, index written); the haystack probes are "
+                       "latency-bound gathers, mostly from L2",
+        "roofline": roofline(12.0 * m, kms["search"], "search (12 B/query)"),
+        "kernel_ms": _rounded(kms), "validated": ok,
+    }
+    del hay_t, q_t, hay, q, out, expect
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -583,10 +618,14 @@ def main():
         _log("compaction")
         cp = run_compaction(torch, np, abi, DeviceBuffer, workloads, args.steps, args.warmup)
         _log("compaction done")
+        _log("search")
+        se = run_search(torch, np, abi, DeviceBuffer, wd, log_sort, max(log_sort - 2, 1),
+                        args.steps, args.warmup)
+        _log("search done")
         out["ordering"] = {"merge": mg, "merge_sort": ms, "set_ops": so, "record_sort": rsr,
-                           "compaction": cp}
+                           "compaction": cp, "lower_bound": se}
         valid = valid and rsr["validated"] and cp["unique_copy"]["validated"] and \
-            cp["reduce_by_key"]["validated"]
+            cp["reduce_by_key"]["validated"] and se["validated"]
         valid = valid and mg["validated"] and ms["validated"] and all(
             so[op]["validated"] for op in ("union", "intersection", "difference",
                                            "symmetric_difference"))

@@ -356,6 +356,27 @@ RCCL_HIP_API rccl_hip_status rccl_hip_reduce_by_key(
     void *out_key_payloads, void *out_values, size_t n, uint64_t *d_group_count,
     void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Vectorized binary search
+ * ------------------------------------------------------------------------ */
+
+/* For each of the m needles, the index in the sorted haystack[0, n) of the
+ * first item not before it (upper == 0: lower_bound, the first i with
+ * !(h[i] < x)) or of the first item after it (upper != 0: upper_bound, the
+ * first i with x < h[i]); n when there is none. Indices are written to
+ * out_indices[0, m) as uint64_t. `<` is the natural order of `key` (or its
+ * reverse when order is DESCENDING); with arity 2..6 and key == U32 the
+ * items are [u32; arity] rows in ascending lexicographic order. The haystack
+ * must be sorted under that order (results are unspecified otherwise, as
+ * with NaN keys). thrust::lower_bound / upper_bound over a range of values
+ * has no counterpart in the reference (CCCL_RUST_CAPABILITY_CHECKLIST.md:107
+ * lists it as missing); its datalog callers search sorted columns. */
+RCCL_HIP_API rccl_hip_status rccl_hip_bound_search(rccl_hip_key_kind key, uint32_t arity,
+                                                   rccl_hip_order order, int upper,
+                                                   const void *haystack, size_t n,
+                                                   const void *needles, size_t m,
+                                                   uint64_t *out_indices, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

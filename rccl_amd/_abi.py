@@ -63,6 +63,7 @@ EXPORTED_SYMBOLS = (
     "rccl_hip_group_workspace_bytes",
     "rccl_hip_unique_copy",
     "rccl_hip_reduce_by_key",
+    "rccl_hip_bound_search",
 )
 
 
@@ -179,6 +180,9 @@ def _declare(lib):
     lib_view.rccl_hip_reduce_by_key.restype = st
     lib_view.rccl_hip_reduce_by_key.argtypes = [st, c.c_uint32, st, sz, vp, vp, vp, vp, vp, vp,
                                                 sz, vp, vp, sz, vp]
+    lib_view.rccl_hip_bound_search.restype = st
+    lib_view.rccl_hip_bound_search.argtypes = [st, c.c_uint32, st, c.c_int, vp, sz, vp, sz, vp,
+                                               vp]
     lib_view.rccl_hip_set_op_arithmetic.restype = st
     lib_view.rccl_hip_set_op_arithmetic.argtypes = [st, st, st, vp, vp, sz, vp, vp, sz, vp, sz, vp,
                                                     vp, sz, vp]

@@ -465,3 +465,40 @@ def reduce_by_key(execution, keys, values, output_keys, output_values, group_cou
         None if okp is None else okp.ptr, outv.ptr, n, group_count.ptr, ws.ptr, nbytes,
         execution.launch().handle))
     execution.synchronize()
+
+
+# ---------------------------------------------------------------------------
+# Vectorized binary search: thrust::lower_bound / upper_bound over a range of
+# values (no counterpart in the reference, CCCL_RUST_CAPABILITY_CHECKLIST.md:107).
+# ---------------------------------------------------------------------------
+def _bound(execution, haystack, needles, output, order, upper):
+    from .record_sort import RowBuffer
+
+    h = haystack.buffer if isinstance(haystack, DeviceView) else haystack
+    q = needles.buffer if isinstance(needles, DeviceView) else needles
+    out = output.buffer if isinstance(output, DeviceView) else output
+    if isinstance(h, RowBuffer):
+        if not isinstance(q, RowBuffer) or q.arity != h.arity:
+            raise TypeError("needles must be rows of the haystack's arity")
+        kind, arity = _abi.KEY_KINDS["u32"], h.arity
+    else:
+        if q.dtype != h.dtype:
+            raise TypeError("needles and haystack must have the same item type")
+        kind, arity = _abi.KEY_KINDS[kind_of(h.dtype)], 1
+    if out.dtype != np.dtype(np.uint64):
+        raise TypeError("bound indices are u64")
+    _capacity("bound-search output", q.len(), out.len())
+    _abi.check(_abi.load().rccl_hip_bound_search(
+        kind, arity, cub.order_code(order), int(upper), h.ptr, h.len(), q.ptr, q.len(), out.ptr,
+        execution.launch().handle))
+    execution.synchronize()
+
+
+def lower_bound(execution, haystack, needles, output, order=ascending):
+    """output[i] = first index j of the sorted haystack with !(h[j] < needles[i])."""
+    _bound(execution, haystack, needles, output, order, False)
+
+
+def upper_bound(execution, haystack, needles, output, order=ascending):
+    """output[i] = first index j of the sorted haystack with needles[i] < h[j]."""
+    _bound(execution, haystack, needles, output, order, True)
