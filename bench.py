@@ -399,7 +399,8 @@ def run_record_sort(torch, np, abi, DeviceBuffer, wd, workloads, steps, warmup):
         "reference_published_ms": {"rccl_sm89": 0.437555, "cub_sm89": 0.445030,
                                    "source": "SRDATALOG_HISA_RCCL_TODO.md:180 (other hardware)"},
         "roofline": roofline(48.0 * n, onesweep_ms,
-                             "record_onesweep, active passes (24 B/row read + 24 B/row write)"),
+                             "record_onesweep, active passes (24 B/row read + 24 B/row write)",
+                             profiled_traffic("record_onesweep_active", 28)),
         "idle_pass_ms": round(sum(idle_ms) / max(len(idle_ms), 1), 4),
         "kernel_ms": _rounded(kms), "validated": ok,
     }
@@ -456,7 +457,9 @@ def run_compaction(torch, np, abi, DeviceBuffer, workloads, steps, warmup):
             "ms_per_step": round(ms, 4), "ms_per_step_min": round(ms_min, 4),
             "roofline": roofline(pb_bytes, kms["group_tile"],
                                  "group_tile (keys" + (" and values" if op else "") +
-                                 " read once, one output per run)"),
+                                 " read once, one output per run)",
+                                 profiled_traffic("group_tile_" + ("reduce" if op else "unique"),
+                                                  28)),
             "kernel_ms": _rounded(kms), "validated": ok,
         }
     res["unique_copy"]["reference_published_ms"] = {
@@ -500,7 +503,8 @@ def run_search(torch, np, abi, DeviceBuffer, wd, log2_hay, log2_q, steps, warmup
         "ms_per_step": round(ms, 4), "ms_per_step_min": round(ms_min, 4),
         "bytes_model": "12 B/query (needle read, index written); the haystack probes are "
                        "latency-bound gathers, mostly from L2",
-        "roofline": roofline(12.0 * m, kms["search"], "search (12 B/query)"),
+        "roofline": roofline(12.0 * m, kms["search"], "search (12 B/query)",
+                             profiled_traffic("search", log2_hay + 2)),
         "kernel_ms": _rounded(kms), "validated": ok,
     }
     del hay_t, q_t, hay, q, out, expect
