@@ -22,12 +22,24 @@ namespace merge {
 
 using ordering::NoValue;
 
-constexpr int THREADS = 256;
+// Tile policy: 256 threads; items per thread by key + value bytes.
+// Overridable at build time for tuning.
+#ifndef RCCL_MERGE_THREADS
+#define RCCL_MERGE_THREADS 256
+#endif
+#ifndef RCCL_MERGE_ITEMS_4B
+#define RCCL_MERGE_ITEMS_4B 16
+#endif
+#ifndef RCCL_MERGE_ITEMS_8B
+#define RCCL_MERGE_ITEMS_8B 12
+#endif
+constexpr int THREADS = RCCL_MERGE_THREADS;
 
 template <class K, class V>
 constexpr int items_for() {
   constexpr size_t bytes = sizeof(K) + (std::is_same<V, NoValue>::value ? 0 : sizeof(V));
-  return bytes <= 4 ? 16 : (bytes <= 8 ? 12 : (bytes <= 16 ? 8 : 6));
+  return bytes <= 4 ? RCCL_MERGE_ITEMS_4B
+                    : (bytes <= 8 ? RCCL_MERGE_ITEMS_8B : (bytes <= 16 ? 8 : 6));
 }
 
 template <class K, class V>
@@ -90,20 +102,27 @@ __device__ __forceinline__ void merge_tile(MergeSmem<K, V, ITEMS> &sm, const K *
   uint32_t ib = d - ia;
   K outk[ITEMS];
   uint32_t src[PAIRS ? ITEMS : 1];
-  using ordering::pick;
-  K ka = ia < la ? sm.keys[ia] : K{};
-  K kb = ib < lb ? sm.keys[la + ib] : K{};
+  if constexpr (ordering::use_merge_network<K, V, ITEMS>()) {
+    const K last = Cmp::last();
+    ordering::network_merge<K, Cmp, ITEMS>(
+        outk, [&](int i) { return ia + i < la ? sm.keys[ia + i] : last; },
+        [&](int i) { return ib + i < lb ? sm.keys[la + ib + i] : last; }, less);
+  } else {
+    using ordering::pick;
+    K ka = ia < la ? sm.keys[ia] : K{};
+    K kb = ib < lb ? sm.keys[la + ib] : K{};
 #pragma unroll
-  for (int k = 0; k < ITEMS; ++k) {
-    const bool take_b = ib < lb && (ia >= la || less(kb, ka));
-    outk[k] = pick(take_b, kb, ka);
-    if constexpr (PAIRS) src[k] = take_b ? la + ib : ia;
-    if (take_b) {
-      ++ib;
-      if (ib < lb) kb = sm.keys[la + ib];
-    } else {
-      ++ia;
-      if (ia < la) ka = sm.keys[ia];
+    for (int k = 0; k < ITEMS; ++k) {
+      const bool take_b = ib < lb && (ia >= la || less(kb, ka));
+      outk[k] = pick(take_b, kb, ka);
+      if constexpr (PAIRS) src[k] = take_b ? la + ib : ia;
+      if (take_b) {
+        ++ib;
+        if (ib < lb) kb = sm.keys[la + ib];
+      } else {
+        ++ia;
+        if (ia < la) ka = sm.keys[ia];
+      }
     }
   }
   V outv_reg[PAIRS ? ITEMS : 1];

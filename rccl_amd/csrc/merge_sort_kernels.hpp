@@ -3,9 +3,9 @@
 // Reference behaviour: rccl-cub/src/merge_sort.rs:140-690 (pass control) and
 // rccl-cub/src/ordering_backend/merge.rs:399-1846 (block sort, partition,
 // merge agents). Design:
-//   block_sort   one block per tile of THREADS*ITEMS keys: each thread sorts
+//   block_sort   one block per tile of BT*ITEMS keys: each thread sorts
 //                its items in registers (stable odd-even transposition),
-//                then log2(THREADS) merge-path rounds in padded LDS double
+//                then log2(BT) merge-path rounds in padded LDS double
 //                the sorted runs; source indices travel with the keys so
 //                values are gathered once at the end
 //   partition    per output tile of a merge pass: the pair of runs it lies
@@ -32,20 +32,37 @@ constexpr size_t tile_items() {
   return merge::tile_items<K, V>();
 }
 
-template <class K, class V, int ITEMS>
+// Block sort threads: keys-only sorts of keys up to 4 bytes sort bigger
+// blocks (fewer merge passes); others use the merge tile. A multiple of
+// THREADS, so that every merge pass's pairs of runs hold whole merge tiles.
+#ifndef RCCL_MERGE_SORT_BLOCK_THREADS_4B
+#define RCCL_MERGE_SORT_BLOCK_THREADS_4B 1024
+#endif
+template <class K, class V>
+constexpr int block_threads() {
+  return (std::is_same<V, NoValue>::value && sizeof(K) <= 4) ? RCCL_MERGE_SORT_BLOCK_THREADS_4B
+                                                            : THREADS;
+}
+template <class K, class V>
+constexpr size_t block_tile_items() {
+  return size_t(block_threads<K, V>()) * items_for<K, V>();
+}
+
+template <class K, class V, int ITEMS, int BT>
 struct BlockSortSmem {
-  static constexpr uint32_t TILE = THREADS * ITEMS;
+  static constexpr uint32_t TILE = BT * ITEMS;
   static constexpr bool PAIRS = !std::is_same<V, NoValue>::value;
   K keys[ordering::padded_size(TILE, ITEMS)];
-  uint16_t idx[ordering::padded_size(TILE, ITEMS)];
+  uint16_t idx[PAIRS ? ordering::padded_size(TILE, ITEMS) : 1];
   typename std::conditional<PAIRS, V, char>::type vals[PAIRS ? TILE : 1];
 };
 
-template <class K, class V, class Cmp, int ITEMS>
-__global__ void __launch_bounds__(THREADS)
+template <class K, class V, class Cmp, int ITEMS, int BT>
+__global__ void __launch_bounds__(BT)
 block_sort_kernel(const K *__restrict__ in, const V *__restrict__ in_v, size_t n,
                   K *__restrict__ out, V *__restrict__ out_v) {
-  using Smem = BlockSortSmem<K, V, ITEMS>;
+  constexpr int THREADS = BT;
+  using Smem = BlockSortSmem<K, V, ITEMS, BT>;
   constexpr bool PAIRS = Smem::PAIRS;
   constexpr uint32_t TILE = Smem::TILE;
   static_assert(TILE <= 65536, "source indices are 16-bit");
@@ -90,13 +107,17 @@ block_sort_kernel(const K *__restrict__ in, const V *__restrict__ in_v, size_t n
     }
   }
 
-  // Merge rounds: runs of `w` items become runs of 2w.
+  // Merge rounds: runs of `w` items become runs of 2w. Source indices are
+  // tracked for pairs only; keys-only sorts of integer keys merge with a
+  // network.
+  constexpr bool NETWORK = ordering::use_merge_network<K, V, ITEMS>();
   for (uint32_t w = ITEMS; w < TILE; w *= 2) {
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       sm.keys[ordering::padded<ITEMS>(first + k)] = key[k];
-      sm.idx[ordering::padded<ITEMS>(first + k)] = static_cast<uint16_t>(idx[k]);
+      if constexpr (PAIRS)
+        sm.idx[ordering::padded<ITEMS>(first + k)] = static_cast<uint16_t>(idx[k]);
     }
     __syncthreads();
     const uint32_t g = first / (2 * w) * (2 * w);
@@ -115,6 +136,19 @@ block_sort_kernel(const K *__restrict__ in, const V *__restrict__ in_v, size_t n
         lo = mid + 1;
     }
     uint32_t ia = lo, ib = d - lo;
+    if constexpr (NETWORK) {
+      const K last = Cmp::last();
+      ordering::network_merge<K, Cmp, ITEMS>(
+          key,
+          [&](int i) {
+            return ia + i < la ? sm.keys[ordering::padded<ITEMS>(a0 + ia + i)] : last;
+          },
+          [&](int i) {
+            return ib + i < lb ? sm.keys[ordering::padded<ITEMS>(b0 + ib + i)] : last;
+          },
+          less);
+      continue;
+    }
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
       const bool a_ok = ia < la, b_ok = ib < lb;
@@ -123,7 +157,7 @@ block_sort_kernel(const K *__restrict__ in, const V *__restrict__ in_v, size_t n
       const K ka = sm.keys[pa], kb = sm.keys[pb];
       const bool take_b = b_ok && (!a_ok || less(kb, ka));
       key[k] = take_b ? kb : ka;
-      idx[k] = take_b ? sm.idx[pb] : sm.idx[pa];
+      if constexpr (PAIRS) idx[k] = take_b ? sm.idx[pb] : sm.idx[pa];
       ib += take_b ? 1u : 0u;
       ia += take_b ? 0u : 1u;
     }
@@ -205,7 +239,7 @@ struct SortArgs {
 };
 
 struct Layout {
-  size_t tiles = 0, passes = 0;
+  size_t tiles = 0, block_tiles = 0, passes = 0;
   size_t scratch_k = 0, scratch_v = 0, splits = 0, total = 0;
 };
 
@@ -214,9 +248,11 @@ Layout layout(size_t n) {
   Layout l;
   if (n == 0) return l;
   constexpr size_t TILE = tile_items<K, V>();
+  constexpr size_t BTILE = block_tile_items<K, V>();
   constexpr size_t VB = std::is_same<V, NoValue>::value ? 0 : sizeof(V);
   l.tiles = (n + TILE - 1) / TILE;
-  while ((size_t(1) << l.passes) < l.tiles) ++l.passes;
+  l.block_tiles = (n + BTILE - 1) / BTILE;
+  while ((size_t(1) << l.passes) < l.block_tiles) ++l.passes;
   size_t off = 0;
   l.scratch_k = off;
   off += align_up(n * sizeof(K), 256);
@@ -232,6 +268,8 @@ template <class K, class V, class Cmp>
 rccl_hip_status run_sort(const SortArgs &s) {
   constexpr int ITEMS = items_for<K, V>();
   constexpr size_t TILE = tile_items<K, V>();
+  constexpr int BT = block_threads<K, V>();
+  static_assert(BT % THREADS == 0, "block sort tiles hold whole merge tiles");
   if (s.n < 1) return ok();
   const Layout l = layout<K, V>(s.n);
   if (!s.ws || s.ws_bytes < l.total)
@@ -244,15 +282,15 @@ rccl_hip_status run_sort(const SortArgs &s) {
   const int first = static_cast<int>(l.passes & 1);
   {
     KernelTimer t("merge_sort_block", s.stream, s.n);
-    block_sort_kernel<K, V, Cmp, ITEMS><<<dim3(static_cast<uint32_t>(l.tiles)), THREADS, 0,
-                                          s.stream>>>(
+    block_sort_kernel<K, V, Cmp, ITEMS, BT><<<dim3(static_cast<uint32_t>(l.block_tiles)), BT, 0,
+                                              s.stream>>>(
         static_cast<const K *>(s.in), static_cast<const V *>(s.in_v), s.n, bufk[first],
         bufv[first]);
   }
   RCCL_HIP_TRY(check_launch("merge sort block"));
   int cur = first;
   for (size_t p = 0; p < l.passes; ++p) {
-    const size_t run = TILE << p;
+    const size_t run = block_tile_items<K, V>() << p;
     {
       KernelTimer t("merge_sort_partition", s.stream, l.tiles);
       pass_partition_kernel<K, Cmp><<<dim3(static_cast<uint32_t>((l.tiles + 255) / 256)), 256, 0,

@@ -3,6 +3,7 @@
 // a runtime (key kind, order, value width) onto compile-time instantiations.
 #pragma once
 
+#include <limits>
 #include <type_traits>
 
 #include "common.hpp"
@@ -22,7 +23,50 @@ struct Less {
     if constexpr (DESC) return b < a;
     else return a < b;
   }
+  // A key no other key comes after (padding for merge networks).
+  __device__ static __forceinline__ K last() {
+    return DESC ? std::numeric_limits<K>::lowest() : std::numeric_limits<K>::max();
+  }
 };
+
+// Keys-only merges of integer keys can use a merge network: equal integer
+// keys are identical bit patterns, so which copy of an equal key lands where
+// cannot be observed and stability holds trivially. (Float keys are left out:
+// -0.0 and +0.0 compare equal but differ in their bits.)
+template <class K, class V, int ITEMS>
+constexpr bool use_merge_network() {
+  return std::is_integral<K>::value && std::is_same<V, NoValue>::value &&
+         (ITEMS & (ITEMS - 1)) == 0;
+}
+
+// The ITEMS first keys, in order, of the merge of two sorted windows: a(i)
+// and b(i) return the windows' i-th keys (Cmp::last() past their ends). The
+// elementwise minimum of a and reversed b is bitonic and holds exactly the
+// ITEMS first keys; a bitonic merge network sorts it. The loads are
+// independent of each other, unlike a serial merge's.
+template <class K, class Cmp, int ITEMS, class LoadA, class LoadB>
+__device__ __forceinline__ void network_merge(K (&out)[ITEMS], LoadA a, LoadB b, Cmp less) {
+  K x[ITEMS], y[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    x[i] = a(i);
+    y[i] = b(ITEMS - 1 - i);
+  }
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) out[i] = less(y[i], x[i]) ? y[i] : x[i];
+#pragma unroll
+  for (int s = ITEMS / 2; s > 0; s >>= 1) {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      if ((i & s) == 0) {
+        const K lo = out[i], hi = out[i + s];
+        const bool swap = less(hi, lo);
+        out[i] = swap ? hi : lo;
+        out[i + s] = swap ? lo : hi;
+      }
+    }
+  }
+}
 
 // Choice between two keys. Aggregate keys (record rows) overload it in their
 // own namespace with a per-word choice, found by argument-dependent lookup, so
