@@ -55,6 +55,23 @@ struct KeyOps {
   }
 };
 
+// Key loads of a keys-only onesweep are non-temporal: they are read once, and
+// leaving L2 to the scattered writes (whose partial lines merge there) and the
+// look-back measured faster. Pair sorts and stores keep the default policy:
+// non-temporal value loads and stores measured slower.
+template <bool NT, class T>
+__device__ __forceinline__ T stream_load(const T *p) {
+  if constexpr (NT && std::is_arithmetic<T>::value)
+    return __builtin_nontemporal_load(p);
+  else
+    return *p;
+}
+
+// The histogram's key loads are non-temporal too (measured faster).
+#ifndef RCCL_RADIX_HIST_NT
+#define RCCL_RADIX_HIST_NT 1
+#endif
+
 // Look-back descriptor: 2 flag bits over a count.
 template <class Desc> struct DescInfo;
 // Flag 3 never appears in memory: it marks a window slot before the start of
@@ -196,7 +213,7 @@ histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__
 #pragma unroll
     for (int j = 0; j < HIST_ITEMS; ++j) {
       const uint32_t i = uint32_t(j) * HIST_THREADS + tid;
-      k[j] = i < avail ? keys[base + i] : Bits(0);
+      k[j] = i < avail ? stream_load<RCCL_RADIX_HIST_NT>(&keys[base + i]) : Bits(0);
     }
 #pragma unroll
     for (int j = 0; j < HIST_ITEMS; ++j) {
@@ -270,7 +287,8 @@ histogram32_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict
     const uint32_t avail = static_cast<uint32_t>(min<size_t>(n - base, CHUNK));
 #pragma unroll
     for (int j = 0; j < HIST32_ITEMS; ++j)
-      next[j] = keys[base + min(uint32_t(j) * HIST32_THREADS + tid, avail - 1u)];
+      next[j] = stream_load<RCCL_RADIX_HIST_NT>(
+          &keys[base + min(uint32_t(j) * HIST32_THREADS + tid, avail - 1u)]);
   };
   if (size_t(blockIdx.x) * CHUNK < n) load_chunk(size_t(blockIdx.x) * CHUNK);
   for (size_t base = size_t(blockIdx.x) * CHUNK; base < n; base += stride) {
@@ -525,7 +543,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   Bits key[ITEMS];
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j)
-    key[j] = keys_in[min(wave_base + size_t(j) * 64 + lane, last_item)];
+    key[j] = stream_load<!PAIRS>(&keys_in[min(wave_base + size_t(j) * 64 + lane, last_item)]);
   ValReg val[ITEMS];
   if constexpr (PAIRS) {
     // Issued now, consumed after the key scatter.
