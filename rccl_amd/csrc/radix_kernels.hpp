@@ -5,8 +5,8 @@
 // kernels are an independent wave64 design:
 //   init        zero the per-pass bins (one tiny block)
 //   histogram   one read of all keys builds every pass's 256-bin histogram in
-//               LDS (per-wave private counters) and adds them to the bins; it
-//               also zeroes look-back buffer 0
+//               LDS (per-lane counter columns) and adds them to the bins;
+//               it also zeroes look-back buffer 0
 //   onesweep    one launch per pass, one tile per block (XCD-aware tile
 //               order); per-wave LDS digit counts, ranking by lane-ordered
 //               returning LDS atomics, a windowed two-level decoupled
@@ -68,6 +68,9 @@ __device__ __forceinline__ T stream_load(const T *p) {
 }
 
 // The histogram's key loads are non-temporal too (measured faster).
+#ifndef RCCL_RADIX_NT_PAIR_KEYS
+#define RCCL_RADIX_NT_PAIR_KEYS 0
+#endif
 #ifndef RCCL_RADIX_HIST_NT
 #define RCCL_RADIX_HIST_NT 1
 #endif
@@ -187,86 +190,43 @@ __global__ void __launch_bounds__(256) init_kernel(uint32_t *bins, uint32_t pass
 // ---------------------------------------------------------------------------
 // histogram: every pass's digit counts from one read of the keys.
 // ---------------------------------------------------------------------------
-constexpr int HIST_THREADS = 512;
-constexpr int HIST_ITEMS = 16;
+// Per-lane counter columns: lane l of every wave counts into column
+// l % cols of its digit's row, so the lanes of one LDS atomic hit at most a
+// few banks' worth of conflicts instead of random ones (random digits into one
+// shared row per wave cost about twice as many LDS cycles per atomic; for
+// 8-byte keys the LDS was busy 69% of the time, half of it in conflicts).
+// All passes' rows take 64 KB (16 columns for 4-byte keys, 8 for 8-byte
+// keys): two blocks per CU, grid-striding over chunks.
+#ifndef RCCL_RADIX_HIST_THREADS
+#define RCCL_RADIX_HIST_THREADS 512
+#endif
+#ifndef RCCL_RADIX_HIST_ITEMS
+#define RCCL_RADIX_HIST_ITEMS 16
+#endif
+#ifndef RCCL_RADIX_HIST_COLS
+#define RCCL_RADIX_HIST_COLS 16
+#endif
+constexpr int HIST_THREADS = RCCL_RADIX_HIST_THREADS;
+constexpr int HIST_ITEMS = RCCL_RADIX_HIST_ITEMS;
+constexpr int HIST_COLS_4B = RCCL_RADIX_HIST_COLS;
+
+template <class Bits>
+constexpr int hist_cols() {
+  return HIST_COLS_4B * 4 / int(sizeof(Bits));
+}
 
 template <class Bits, class Ops>
 __global__ void __launch_bounds__(HIST_THREADS)
 histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__ bins,
                  uint32_t begin_bit, uint32_t end_bit, uint32_t passes,
                  uint32_t *__restrict__ zero_words, size_t zero_count) {
-  constexpr int WAVES = HIST_THREADS / 64;
-  constexpr int PMAX = sizeof(Bits);
-  __shared__ uint32_t hist[WAVES][PMAX * BINS];
-  const uint32_t tid = threadIdx.x;
-  for (uint32_t i = tid; i < WAVES * PMAX * BINS; i += HIST_THREADS) (&hist[0][0])[i] = 0;
-  for (size_t i = size_t(blockIdx.x) * HIST_THREADS + tid; i < zero_count;
-       i += size_t(gridDim.x) * HIST_THREADS)
-    zero_words[i] = 0;
-  __syncthreads();
-
-  uint32_t *my = hist[tid >> 6];
-  constexpr size_t CHUNK = size_t(HIST_THREADS) * HIST_ITEMS;
-  for (size_t base = size_t(blockIdx.x) * CHUNK; base < n; base += size_t(gridDim.x) * CHUNK) {
-    Bits k[HIST_ITEMS];
-    const uint32_t avail = static_cast<uint32_t>(min<size_t>(n - base, CHUNK));
-#pragma unroll
-    for (int j = 0; j < HIST_ITEMS; ++j) {
-      const uint32_t i = uint32_t(j) * HIST_THREADS + tid;
-      k[j] = i < avail ? stream_load<RCCL_RADIX_HIST_NT>(&keys[base + i]) : Bits(0);
-    }
-#pragma unroll
-    for (int j = 0; j < HIST_ITEMS; ++j) {
-      if (uint32_t(j) * HIST_THREADS + tid >= avail) continue;
-      const Bits s = Ops::digit_source(k[j]);
-      for (uint32_t p = 0; p < passes; ++p) {
-        const uint32_t bit = begin_bit + 8u * p;
-        const uint32_t width = min(8u, end_bit - bit);
-        const uint32_t d = static_cast<uint32_t>(s >> bit) & ((1u << width) - 1u);
-        atomicAdd(&my[p * BINS + d], 1u);
-      }
-    }
-  }
-  __syncthreads();
-  for (uint32_t i = tid; i < passes * BINS; i += HIST_THREADS) {
-    uint32_t sum = 0;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) sum += hist[w][i];
-    if (sum) add_agent(&bins[i], sum);
-  }
-}
-
-// histogram32: the same for 4-byte keys, with per-lane counter columns. Lane
-// l of every wave counts into column l % HIST_COLS of its digit's row, so the
-// lanes of one LDS atomic hit at most two banks' worth of conflicts instead of
-// random ones (random digits into one shared row per wave cost about twice as
-// many LDS cycles per atomic). All four passes' rows take 64 KB: two blocks
-// per CU, grid-striding over chunks.
-#ifndef RCCL_RADIX_HIST32_THREADS
-#define RCCL_RADIX_HIST32_THREADS 512
-#endif
-#ifndef RCCL_RADIX_HIST32_ITEMS
-#define RCCL_RADIX_HIST32_ITEMS 16
-#endif
-#ifndef RCCL_RADIX_HIST_COLS
-#define RCCL_RADIX_HIST_COLS 16
-#endif
-constexpr int HIST32_THREADS = RCCL_RADIX_HIST32_THREADS;
-constexpr int HIST32_ITEMS = RCCL_RADIX_HIST32_ITEMS;
-constexpr int HIST_COLS = RCCL_RADIX_HIST_COLS;
-
-template <class Bits, class Ops>
-__global__ void __launch_bounds__(HIST32_THREADS)
-histogram32_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__ bins,
-                   uint32_t begin_bit, uint32_t end_bit, uint32_t passes,
-                   uint32_t *__restrict__ zero_words, size_t zero_count) {
-  static_assert(sizeof(Bits) == 4, "4-byte keys: at most four 8-bit passes");
-  constexpr int PMAX = 4;
+  constexpr int PMAX = int(sizeof(Bits));  // 8-bit passes
+  constexpr int HIST_COLS = hist_cols<Bits>();
   __shared__ uint32_t hist[PMAX * BINS * HIST_COLS];  // [pass][digit][column]
   const uint32_t tid = threadIdx.x;
-  for (uint32_t i = tid; i < passes * BINS * HIST_COLS; i += HIST32_THREADS) hist[i] = 0;
-  for (size_t i = size_t(blockIdx.x) * HIST32_THREADS + tid; i < zero_count;
-       i += size_t(gridDim.x) * HIST32_THREADS)
+  for (uint32_t i = tid; i < passes * BINS * HIST_COLS; i += HIST_THREADS) hist[i] = 0;
+  for (size_t i = size_t(blockIdx.x) * HIST_THREADS + tid; i < zero_count;
+       i += size_t(gridDim.x) * HIST_THREADS)
     zero_words[i] = 0;
   __syncthreads();
 
@@ -280,26 +240,26 @@ histogram32_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict
   }
   // The next chunk's keys are loaded before the current chunk is counted, so
   // the load latency hides behind the counting.
-  constexpr size_t CHUNK = size_t(HIST32_THREADS) * HIST32_ITEMS;
+  constexpr size_t CHUNK = size_t(HIST_THREADS) * HIST_ITEMS;
   const size_t stride = size_t(gridDim.x) * CHUNK;
-  Bits next[HIST32_ITEMS];
+  Bits next[HIST_ITEMS];
   auto load_chunk = [&](size_t base) {
     const uint32_t avail = static_cast<uint32_t>(min<size_t>(n - base, CHUNK));
 #pragma unroll
-    for (int j = 0; j < HIST32_ITEMS; ++j)
+    for (int j = 0; j < HIST_ITEMS; ++j)
       next[j] = stream_load<RCCL_RADIX_HIST_NT>(
-          &keys[base + min(uint32_t(j) * HIST32_THREADS + tid, avail - 1u)]);
+          &keys[base + min(uint32_t(j) * HIST_THREADS + tid, avail - 1u)]);
   };
   if (size_t(blockIdx.x) * CHUNK < n) load_chunk(size_t(blockIdx.x) * CHUNK);
   for (size_t base = size_t(blockIdx.x) * CHUNK; base < n; base += stride) {
     const uint32_t avail = static_cast<uint32_t>(min<size_t>(n - base, CHUNK));
-    Bits k[HIST32_ITEMS];
+    Bits k[HIST_ITEMS];
 #pragma unroll
-    for (int j = 0; j < HIST32_ITEMS; ++j) k[j] = next[j];
+    for (int j = 0; j < HIST_ITEMS; ++j) k[j] = next[j];
     if (base + stride < n) load_chunk(base + stride);
 #pragma unroll
-    for (int j = 0; j < HIST32_ITEMS; ++j) {
-      if (uint32_t(j) * HIST32_THREADS + tid >= avail) continue;
+    for (int j = 0; j < HIST_ITEMS; ++j) {
+      if (uint32_t(j) * HIST_THREADS + tid >= avail) continue;
       const Bits s = Ops::digit_source(k[j]);
 #pragma unroll
       for (int p = 0; p < PMAX; ++p) {
@@ -313,7 +273,7 @@ histogram32_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict
   __syncthreads();
   // Row sums. Thread e reads its row's columns in rotated order, so the
   // threads of a wave read distinct banks.
-  for (uint32_t e = tid; e < passes * BINS; e += HIST32_THREADS) {
+  for (uint32_t e = tid; e < passes * BINS; e += HIST_THREADS) {
     const uint32_t *row = &hist[e * HIST_COLS];
     uint32_t sum = 0;
 #pragma unroll
@@ -543,7 +503,8 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   Bits key[ITEMS];
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j)
-    key[j] = stream_load<!PAIRS>(&keys_in[min(wave_base + size_t(j) * 64 + lane, last_item)]);
+    key[j] = stream_load<!PAIRS || RCCL_RADIX_NT_PAIR_KEYS>(
+        &keys_in[min(wave_base + size_t(j) * 64 + lane, last_item)]);
   ValReg val[ITEMS];
   if constexpr (PAIRS) {
     // Issued now, consumed after the key scatter.
@@ -778,23 +739,15 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
   }
   {
     KernelTimer t("radix_histogram", a.stream, a.n);
-    if constexpr (sizeof(Bits) == 4) {
-      const size_t chunk = size_t(HIST32_THREADS) * HIST32_ITEMS;
-      const size_t per_cu = (160 * 1024) / (4 * BINS * HIST_COLS * sizeof(uint32_t));
-      const size_t blocks = std::max<size_t>(
-          1, std::min<size_t>((a.n + chunk - 1) / chunk, size_t(hist_cus) * per_cu));
-      histogram32_kernel<Bits, Ops><<<dim3(static_cast<uint32_t>(blocks)), HIST32_THREADS, 0,
-                                      a.stream>>>(
-          static_cast<const Bits *>(a.keys[a.cur]), a.n, bins, a.begin_bit, a.end_bit, passes,
-          reinterpret_cast<uint32_t *>(a.ws + l.lb[0]), zero_words);
-    } else {
-      const size_t chunk = size_t(HIST_THREADS) * HIST_ITEMS;
-      const size_t blocks = std::max<size_t>(1, std::min<size_t>((a.n + chunk - 1) / chunk, 2048));
-      histogram_kernel<Bits, Ops><<<dim3(static_cast<uint32_t>(blocks)), HIST_THREADS, 0,
-                                    a.stream>>>(
-          static_cast<const Bits *>(a.keys[a.cur]), a.n, bins, a.begin_bit, a.end_bit, passes,
-          reinterpret_cast<uint32_t *>(a.ws + l.lb[0]), zero_words);
-    }
+    const size_t chunk = size_t(HIST_THREADS) * HIST_ITEMS;
+    const size_t per_cu =
+        (160 * 1024) / (sizeof(Bits) * BINS * hist_cols<Bits>() * sizeof(uint32_t));
+    const size_t blocks = std::max<size_t>(
+        1, std::min<size_t>((a.n + chunk - 1) / chunk, size_t(hist_cus) * per_cu));
+    histogram_kernel<Bits, Ops><<<dim3(static_cast<uint32_t>(blocks)), HIST_THREADS, 0,
+                                  a.stream>>>(
+        static_cast<const Bits *>(a.keys[a.cur]), a.n, bins, a.begin_bit, a.end_bit, passes,
+        reinterpret_cast<uint32_t *>(a.ws + l.lb[0]), zero_words);
   }
   RCCL_HIP_TRY(check_launch("radix histogram"));
   {
