@@ -103,4 +103,21 @@ __device__ __forceinline__ T wave_inclusive_sum(T v, uint32_t lane) {
   return v;
 }
 
+// 32-bit inclusive sum over a full wave64 in DPP moves, with no LDS round
+// trip: each row of 16 lanes scans with row shifts of 1, 2, 4 and 8 (lanes
+// shifted in from outside the row read 0), row_bcast:15 adds the last lane of
+// rows 0 and 2 to rows 1 and 3, and row_bcast:31 adds lane 31 (the total of
+// rows 0 and 1) to rows 2 and 3. Every lane of the wave must be active.
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v, uint32_t) {
+  constexpr int ROW_SHR = 0x110, ROW_BCAST15 = 0x142, ROW_BCAST31 = 0x143;
+  int x = static_cast<int>(v);
+  x += __builtin_amdgcn_update_dpp(0, x, ROW_SHR + 1, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, ROW_SHR + 2, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, ROW_SHR + 4, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, ROW_SHR + 8, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, ROW_BCAST15, 0xa, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, ROW_BCAST31, 0xc, 0xf, false);
+  return static_cast<uint32_t>(x);
+}
+
 } // namespace rccl_hip

@@ -606,13 +606,21 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     stage_keys[pos[j]] = key[j];
   }
 
+  // All loads (the look-back windows included) are complete on both sides of
+  // this branch before the prefix stores. Without that the compiler cannot
+  // tell at the join which loads may still be in flight, and makes the
+  // scatter wait for every outstanding operation, the prefix stores' round
+  // trip included.
   if (tid < BINS) {
     const Desc excl = lookback_consume<Desc>(lbuf, tile, group, tid, lb, gi, ga);
+    wait_vmcnt<0>();
     const Desc incl = static_cast<Desc>(DI::INCL | (excl + Desc(count)));
     if (tile > 0) store_agent(&lbuf.tile[size_t(tile) * BINS + tid], incl);
     const uint32_t glast = min(uint32_t(gfirst + GROUP), num_tiles) - 1u;
     if (tile == glast) store_agent(&lbuf.ginc[size_t(group) * BINS + tid], incl);
     digit_off[tid] = bin_start + static_cast<uint32_t>(excl) - tile_start;
+  } else {
+    wait_vmcnt<0>();
   }
   lds_barrier();
 
