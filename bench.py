@@ -279,20 +279,38 @@ def run_merge_sort(torch, np, cub, abi, DeviceBuffer, wd, log2n, steps, warmup):
     ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, launch.stream(), steps, warmup, step)
     ok = _nondecreasing(torch, out.tensor, 32)
     ok = ok and _fingerprint(torch, out.tensor) == _fingerprint(torch, keys_t)
-    passes = launches.get("merge_sort_pass", 0)
     res = {
         "workload": f"C4 DeviceMergeSort keys: 2^{log2n} u32 keys in [0, 2^24), ascending "
                     "(copy form: input left untouched)",
         "value": round(n / (ms * 1e-3) / 1e9, 3), "unit": "Gkeys/s",
         "ms_per_step": round(ms, 4), "ms_per_step_wall": round(wall, 4),
-        "merge_passes": passes,
-        "bytes_model": f"{8 * (1 + passes)} B/key = 8 B (block sort) + 8 B per merge pass",
-        "roofline": roofline(8.0 * n, kms["merge_sort_pass"],
-                             "merge_sort_pass (one pass: 4n read + 4n write)",
-                             profiled_traffic("merge_sort_pass", log2n + 2)),
-        "sort_roofline_frac": round(8.0 * (1 + passes) * n / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "kernel_ms": _rounded(kms), "validated": bool(ok),
     }
+    if "radix_onesweep" in kms:
+        # Integer keys lower to the stable radix sort (same permutation).
+        passes = launches.get("radix_onesweep", 0)
+        key_bytes = 4 + 8 * passes
+        res.update({
+            "lowering": "stable LSD radix sort (integer keys, natural order)",
+            "radix_passes": passes,
+            "bytes_model": f"{key_bytes} B/key = 4 B (histogram) + 8 B per radix pass",
+            "roofline": roofline(8.0 * n, kms["radix_onesweep"],
+                                 "radix_onesweep (one pass: 4n read + 4n write)",
+                                 profiled_traffic("merge_sort_radix_onesweep", log2n + 2)),
+        })
+    else:
+        passes = launches.get("merge_sort_pass", 0)
+        key_bytes = 8 * (1 + passes)
+        res.update({
+            "merge_passes": passes,
+            "bytes_model": f"{key_bytes} B/key = 8 B (block sort) + 8 B per merge pass",
+            "roofline": roofline(8.0 * n, kms["merge_sort_pass"],
+                                 "merge_sort_pass (one pass: 4n read + 4n write)",
+                                 profiled_traffic("merge_sort_pass", log2n + 2)),
+        })
+    res.update({
+        "sort_roofline_frac": round(key_bytes * n / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "kernel_ms": _rounded(kms), "validated": bool(ok),
+    })
     del keys_t, src, out, ws
     torch.cuda.empty_cache()
     return res

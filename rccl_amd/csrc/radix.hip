@@ -140,6 +140,51 @@ size_t single_tile_items(size_t key_bytes_, size_t value_bytes) {
 }
 
 } // namespace
+
+size_t merge_sort_lowering_bytes(size_t key_bytes_, size_t value_bytes, size_t n) {
+  return align_up(n * key_bytes_, 256) + align_up(n * value_bytes, 256) +
+         layout(key_bytes_, value_bytes, n).total;
+}
+
+// A stable LSD radix sort of integer keys under the natural order or its
+// reverse yields exactly the stable merge sort's permutation: digit order is
+// integer order, and equal keys keep their input order. The output buffers
+// are the first half of the double buffer and the workspace's scratch the
+// second; a copy form reads its input in the histogram and the first pass
+// only. Keys of 4 and 8 bytes take 4 and 8 passes, an even count, so the
+// result ends in the output buffers.
+rccl_hip_status merge_sort_lowering(rccl_hip_key_kind key, size_t value_bytes, bool descending,
+                                    const void *in_keys, const void *in_vals, void *out_keys,
+                                    void *out_vals, size_t n, void *workspace,
+                                    size_t workspace_bytes, hipStream_t stream) {
+  const size_t kb = key_bytes(key);
+  if (key != RCCL_HIP_KEY_U32 && key != RCCL_HIP_KEY_I32 && key != RCCL_HIP_KEY_U64 &&
+      key != RCCL_HIP_KEY_I64)
+    return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "merge sort radix key kind");
+  const size_t scratch = align_up(n * kb, 256) + align_up(n * value_bytes, 256);
+  if (!workspace || workspace_bytes < merge_sort_lowering_bytes(kb, value_bytes, n))
+    return set_error(RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL, "merge sort workspace",
+                     merge_sort_lowering_bytes(kb, value_bytes, n), workspace_bytes);
+  unsigned char *ws = static_cast<unsigned char *>(workspace);
+  SortArgs a{};
+  a.keys[0] = out_keys;
+  a.keys[1] = ws;
+  a.vals[0] = value_bytes ? out_vals : nullptr;
+  a.vals[1] = value_bytes ? ws + align_up(n * kb, 256) : nullptr;
+  a.n = n;
+  a.cur = 0;
+  a.begin_bit = 0;
+  a.end_bit = static_cast<uint32_t>(kb * 8);
+  a.ws = ws + scratch;
+  a.stream = stream;
+  if (in_keys != out_keys || (value_bytes && in_vals != out_vals)) {
+    a.src_keys = in_keys;
+    a.src_vals = value_bytes ? in_vals : nullptr;
+  }
+  return sort_buffer(key, value_bytes,
+                     descending ? RCCL_HIP_ORDER_DESCENDING : RCCL_HIP_ORDER_ASCENDING, a,
+                     workspace_bytes - scratch);
+}
 } // namespace radix
 } // namespace rccl_hip
 

@@ -452,6 +452,11 @@ __device__ __forceinline__ void launder(T &x) {
   asm volatile("" : "+v"(x));
 }
 
+// True when every lane of the (fully active) wave holds the same value.
+__device__ __forceinline__ bool wave_uniform(uint32_t v) {
+  return __ballot(v == __builtin_amdgcn_readfirstlane(v)) == ~uint64_t(0);
+}
+
 // One tile of a onesweep pass. Keys are any trivially copyable type whose
 // digits Ops::digit extracts (scalar keys, or record rows); the kernels below
 // wrap it.
@@ -520,13 +525,21 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   // with the counting atomics.
   wait_vmcnt<PAIRS ? ITEMS : 0>();
 
-  // Per-wave digit counts.
+  // Per-wave digit counts. Lanes of one LDS atomic that hit the same counter
+  // are served one after another, so an item whose digit is the same in all
+  // 64 lanes (skewed or presorted keys, a constant byte) is counted by one
+  // lane adding 64.
   uint32_t *wcnt = cnt[wave];
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) {
     const uint32_t d =
         uint32_t(j) * 64 + lane < wave_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
-    __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (wave_uniform(d)) {
+      if (lane == 0)
+        __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+      __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
   }
   lds_barrier();
 
@@ -591,17 +604,29 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   // All atomics are issued before the first staging write, so the round
   // trips overlap; the opaque copy of the positions keeps the compiler from
   // pairing each write with its atomic (which serialises them).
+  // A wave-uniform digit takes 64 consecutive positions with one atomic:
+  // lane l's is the returned base + l, as the lane-ordered atomic would give.
   uint32_t pos[ITEMS];
+  uint64_t uniform = 0;
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) {
     const uint32_t d =
         uint32_t(j) * 64 + lane < wave_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
-    pos[j] = __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (wave_uniform(d)) {
+      uniform |= uint64_t(1) << j;
+      pos[j] = lane == 0 ? __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_WORKGROUP)
+                         : 0u;
+    } else {
+      pos[j] =
+          __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
   }
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) asm volatile("" : "+v"(pos[j]));
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) {
+    if (uniform & (uint64_t(1) << j)) pos[j] = __builtin_amdgcn_readfirstlane(pos[j]) + lane;
     pos[j] = min(pos[j], uint32_t(TILE));
     stage_keys[pos[j]] = key[j];
   }
@@ -714,6 +739,11 @@ struct SortArgs {
   uint32_t begin_bit, end_bit;
   unsigned char *ws;
   hipStream_t stream;
+  // When set, the histogram and the first pass read the input from here
+  // instead of keys[cur] / vals[cur], which then only receive output: sorts
+  // that must leave their input untouched start without a copy.
+  const void *src_keys = nullptr;
+  const void *src_vals = nullptr;
 };
 
 template <class Bits, class Val, class Ops, class Desc>
@@ -754,7 +784,8 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
         1, std::min<size_t>((a.n + chunk - 1) / chunk, size_t(hist_cus) * per_cu));
     histogram_kernel<Bits, Ops><<<dim3(static_cast<uint32_t>(blocks)), HIST_THREADS, 0,
                                   a.stream>>>(
-        static_cast<const Bits *>(a.keys[a.cur]), a.n, bins, a.begin_bit, a.end_bit, passes,
+        static_cast<const Bits *>(a.src_keys ? a.src_keys : a.keys[a.cur]), a.n, bins,
+        a.begin_bit, a.end_bit, passes,
         reinterpret_cast<uint32_t *>(a.ws + l.lb[0]), zero_words);
   }
   RCCL_HIP_TRY(check_launch("radix histogram"));
@@ -787,10 +818,13 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
     const uint32_t width = std::min(8u, a.end_bit - bit);
     const uint32_t mask = (1u << width) - 1u;
     const int in = a.cur, out = 1 - a.cur;
+    const bool from_src = p == 0 && a.src_keys;
+    const void *kin = from_src ? a.src_keys : a.keys[in];
+    const void *vin = from_src ? a.src_vals : a.vals[in];
     KernelTimer t("radix_onesweep", a.stream, a.n);
     onesweep_kernel<Bits, Val, Ops, ITEMS, Desc, THREADS><<<dim3(grid), THREADS, 0, a.stream>>>(
-        static_cast<const Bits *>(a.keys[in]), static_cast<Bits *>(a.keys[out]),
-        static_cast<const Val *>(a.vals[in]), static_cast<Val *>(a.vals[out]), a.n,
+        static_cast<const Bits *>(kin), static_cast<Bits *>(a.keys[out]),
+        static_cast<const Val *>(vin), static_cast<Val *>(a.vals[out]), a.n,
         static_cast<uint32_t>(l.tiles), bins + size_t(p) * BINS, lb[p & 1],
         p + 1 < passes ? lb[(p + 1) & 1] : LookbackBuf<Desc>{nullptr, nullptr, nullptr}, bit,
         mask);
@@ -825,6 +859,14 @@ rccl_hip_status run_values(SortArgs &a, size_t value_bytes, const Layout &l, uin
   }
   return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix value bytes");
 }
+
+// DeviceMergeSort over integer keys lowers to this stable radix sort (see
+// radix.hip). Workspace: scratch keys and values, then the radix layout.
+size_t merge_sort_lowering_bytes(size_t key_bytes, size_t value_bytes, size_t n);
+rccl_hip_status merge_sort_lowering(rccl_hip_key_kind key, size_t value_bytes, bool descending,
+                                    const void *in_keys, const void *in_vals, void *out_keys,
+                                    void *out_vals, size_t n, void *workspace,
+                                    size_t workspace_bytes, hipStream_t stream);
 
 // Runs lane_order_check_kernel once on the current device (see the onesweep
 // notes); RCCL_HIP_ERROR_UNSUPPORTED_TARGET if the LDS does not serve lanes of

@@ -248,6 +248,27 @@ def test_workspace_sizes_scale(lib):
     assert ms >= (1 << 20) * 8  # scratch keys and values
 
 
+@pytest.mark.parametrize("key,kb", [(0, 4), (1, 4), (3, 8), (4, 8)])
+@pytest.mark.parametrize("vb", [0, 4, 16])
+def test_merge_sort_radix_lowering_workspace(lib, key, kb, vb):
+    """Integer merge sorts from 65,536 items run as a radix sort: the
+    workspace covers the scratch keys and values plus the radix control
+    state; below the threshold and for float keys it is the merge sort's."""
+    def align(x):
+        return (x + 255) // 256 * 256
+    for n in (65_536, 1 << 22):
+        ms = _abi.workspace_bytes("rccl_hip_merge_sort_workspace_bytes", key, vb, n)
+        radix = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", key, vb, n)
+        assert ms >= align(n * kb) + align(n * vb) + radix
+        # Below the threshold: the merge sort's own workspace, no radix state.
+        assert _abi.workspace_bytes("rccl_hip_merge_sort_workspace_bytes", key, vb, 65_535) < \
+            align(65_535 * kb) + align(65_535 * vb) + radix
+    # Too small a workspace fails before any launch.
+    need = _abi.workspace_bytes("rccl_hip_merge_sort_workspace_bytes", key, vb, 70_000)
+    assert lib.rccl_hip_merge_sort(key, vb, 0, FAKE, FAKE if vb else None, FAKE,
+                                   FAKE if vb else None, 70_000, FAKE, need - 1, None) == 2
+
+
 def test_python_mirror_host_logic():
     assert cub.order_code(None) == cub.ASCENDING
     assert cub.order_code(cub.descending) == cub.DESCENDING

@@ -242,3 +242,45 @@ def test_merge_sort_c4_scaled(launch):
     keys = workloads.c4_merge_sort_keys(1 << 21)
     got = _merge_sort(launch, keys)
     assert np.array_equal(got, oracle.merge_sort("u32", keys))
+
+
+@pytest.mark.parametrize("kind", ["u32", "i32", "u64", "i64"])
+def test_merge_sort_radix_lowering(launch, kind):
+    """From 65,536 items, integer keys sort through the stable radix lowering.
+    Sizes on both sides of that threshold, ties (stability, with payloads
+    recording the input order), both orders, in-place and copy forms."""
+    for idx, n in enumerate([65_535, 65_536, 300_007]):
+        for descending in (False, True):
+            keys = _random_keys(kind, n, 1000 + idx, None if idx == 1 else 97)
+            want = oracle.merge_sort(kind, keys, descending=descending)
+            got = _merge_sort(launch, keys, descending=descending, copy=bool(idx % 2))
+            assert np.array_equal(_bits(got), _bits(want)), (kind, n, descending)
+            for width in (4, 16):
+                vals = _values(width, n, 1100 + idx) if width == 16 else \
+                    np.arange(n, dtype=np.uint32)
+                wk, wv = oracle.merge_sort(kind, keys, vals, descending)
+                copy = not bool(idx % 2)
+                k, v = _dev(keys), _dev(vals)
+                ws = cub.device_merge_sort_pairs_workspace(launch, keys.dtype, vals.dtype, n)
+                if copy:
+                    ok = DeviceBuffer.empty(keys.dtype, n)
+                    ov = DeviceBuffer.empty(vals.dtype, n)
+                    cub.device_merge_sort_pairs_copy(launch, k, v, ws, ok, ov, _order(descending))
+                else:
+                    ok, ov = k, v
+                    cub.device_merge_sort_pairs(launch, k, v, ws, _order(descending))
+                launch.synchronize()
+                assert np.array_equal(_bits(ok.to_host_vec()), _bits(wk)), (kind, n, width)
+                assert ov.to_host_vec().tobytes() == wv.tobytes(), (kind, n, width)
+                if copy:
+                    assert np.array_equal(_bits(k.to_host_vec()), _bits(keys)), "input modified"
+                    assert v.to_host_vec().tobytes() == vals.tobytes(), "input modified"
+
+
+def test_merge_sort_c4_full_size(launch):
+    """The benchmark's C4 merge sort (2^26 u32 keys in [0, 2^24), copy form),
+    bit-exact with numpy's stable sort (keys only, so any correct sort is the
+    stable one)."""
+    keys = workloads.c4_merge_sort_keys(1 << 26)
+    got = _merge_sort(launch, keys, copy=True)
+    assert np.array_equal(got, np.sort(keys, kind="stable"))
