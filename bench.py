@@ -505,10 +505,12 @@ def run_search(torch, np, abi, DeviceBuffer, wd, log2_hay, log2_q, steps, warmup
     out = DeviceBuffer.empty(np.uint64, m)
     stream = torch.cuda.current_stream(0)
     lib = abi.load()
+    ws_bytes = abi.workspace_bytes("rccl_hip_bound_search_workspace_bytes", 0, 1, n)
+    ws = DeviceBuffer.bytes(ws_bytes)
 
     def step():
-        abi.check(lib.rccl_hip_bound_search(0, 1, 0, 0, hay.ptr, n, q.ptr, m, out.ptr,
-                                            stream.cuda_stream))
+        abi.check(lib.rccl_hip_bound_search(0, 1, 0, 0, hay.ptr, n, q.ptr, m, out.ptr, ws.ptr,
+                                            ws_bytes, stream.cuda_stream))
 
     ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, stream, steps, warmup, step)
     # Validate against torch.searchsorted on the device (same definition).
@@ -519,13 +521,14 @@ def run_search(torch, np, abi, DeviceBuffer, wd, log2_hay, log2_q, steps, warmup
                     "haystack (values in [0, 2^24))",
         "value": round(m / (ms * 1e-3) / 1e9, 3), "unit": "Gqueries/s",
         "ms_per_step": round(ms, 4), "ms_per_step_min": round(ms_min, 4),
-        "bytes_model": "12 B/query (needle read, index written); the haystack probes are "
-                       "latency-bound gathers, mostly from L2",
+        "bytes_model": "12 B/query (needle read, index written); the per-call chunk index "
+                       "(search_index: one read of the haystack) and the probes, one "
+                       "haystack cache line per query, come on top",
         "roofline": roofline(12.0 * m, kms["search"], "search (12 B/query)",
                              profiled_traffic("search", log2_hay + 2)),
         "kernel_ms": _rounded(kms), "validated": ok,
     }
-    del hay_t, q_t, hay, q, out, expect
+    del hay_t, q_t, hay, q, out, expect, ws
     torch.cuda.empty_cache()
     return res
 

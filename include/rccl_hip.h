@@ -370,12 +370,24 @@ RCCL_HIP_API rccl_hip_status rccl_hip_reduce_by_key(
  * must be sorted under that order (results are unspecified otherwise, as
  * with NaN keys). thrust::lower_bound / upper_bound over a range of values
  * has no counterpart in the reference (CCCL_RUST_CAPABILITY_CHECKLIST.md:107
- * lists it as missing); its datalog callers search sorted columns. */
+ * lists it as missing); its datalog callers search sorted columns.
+ * The workspace (rccl_hip_bound_search_workspace_bytes) holds a per-call
+ * index of the haystack's cache-line chunks, built when there are enough
+ * needles to repay it; WORKSPACE_TOO_SMALL when such a call's is short. */
 RCCL_HIP_API rccl_hip_status rccl_hip_bound_search(rccl_hip_key_kind key, uint32_t arity,
                                                    rccl_hip_order order, int upper,
                                                    const void *haystack, size_t n,
                                                    const void *needles, size_t m,
-                                                   uint64_t *out_indices, hipStream_t stream);
+                                                   uint64_t *out_indices, void *workspace,
+                                                   size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes for bound searches in a haystack of n items of `key` (or
+ * [u32; arity] rows): the chunk index, one item per 128 bytes of haystack,
+ * or 0 when the haystack is small enough to need none. No counterpart in
+ * the reference (see rccl_hip_bound_search). */
+RCCL_HIP_API rccl_hip_status rccl_hip_bound_search_workspace_bytes(rccl_hip_key_kind key,
+                                                                   uint32_t arity, size_t n,
+                                                                   size_t *bytes);
 
 #ifdef __cplusplus
 }

@@ -64,6 +64,7 @@ EXPORTED_SYMBOLS = (
     "rccl_hip_unique_copy",
     "rccl_hip_reduce_by_key",
     "rccl_hip_bound_search",
+    "rccl_hip_bound_search_workspace_bytes",
 )
 
 
@@ -182,7 +183,9 @@ def _declare(lib):
                                                 sz, vp, vp, sz, vp]
     lib_view.rccl_hip_bound_search.restype = st
     lib_view.rccl_hip_bound_search.argtypes = [st, c.c_uint32, st, c.c_int, vp, sz, vp, sz, vp,
-                                               vp]
+                                               vp, sz, vp]
+    lib_view.rccl_hip_bound_search_workspace_bytes.restype = st
+    lib_view.rccl_hip_bound_search_workspace_bytes.argtypes = [st, c.c_uint32, sz, c.POINTER(sz)]
     lib_view.rccl_hip_set_op_arithmetic.restype = st
     lib_view.rccl_hip_set_op_arithmetic.argtypes = [st, st, st, vp, vp, sz, vp, vp, sz, vp, sz, vp,
                                                     vp, sz, vp]

@@ -38,19 +38,60 @@ rccl_hip_status dispatch(rccl_hip_key_kind key, uint32_t arity, bool desc,
   return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "search key kind");
 }
 
-} // namespace
+// Workspace bytes of the chunk index for a haystack of n keys (or rows).
+size_t index_bytes(rccl_hip_key_kind key, uint32_t arity, size_t n) {
+  if (arity > 1) {
+    switch (arity) {
+    case 2: return search::workspace_bytes<record_sort::Row<2>>(n);
+    case 3: return search::workspace_bytes<record_sort::Row<3>>(n);
+    case 4: return search::workspace_bytes<record_sort::Row<4>>(n);
+    case 5: return search::workspace_bytes<record_sort::Row<5>>(n);
+    default: return search::workspace_bytes<record_sort::Row<6>>(n);
+    }
+  }
+  switch (key) {
+  case RCCL_HIP_KEY_U32: return search::workspace_bytes<uint32_t>(n);
+  case RCCL_HIP_KEY_I32: return search::workspace_bytes<int32_t>(n);
+  case RCCL_HIP_KEY_F32: return search::workspace_bytes<float>(n);
+  case RCCL_HIP_KEY_U64: return search::workspace_bytes<uint64_t>(n);
+  case RCCL_HIP_KEY_I64: return search::workspace_bytes<int64_t>(n);
+  case RCCL_HIP_KEY_F64: return search::workspace_bytes<double>(n);
+  case RCCL_HIP_KEY_U8: return search::workspace_bytes<uint8_t>(n);
+  case RCCL_HIP_KEY_I8: return search::workspace_bytes<int8_t>(n);
+  case RCCL_HIP_KEY_U16: return search::workspace_bytes<uint16_t>(n);
+  case RCCL_HIP_KEY_I16: return search::workspace_bytes<int16_t>(n);
+  }
+  return 0;
+}
 
-extern "C" {
-
-rccl_hip_status rccl_hip_bound_search(rccl_hip_key_kind key, uint32_t arity, rccl_hip_order order,
-                                      int upper, const void *haystack, size_t n,
-                                      const void *needles, size_t m, uint64_t *out_indices,
-                                      hipStream_t stream) {
+rccl_hip_status check_key(rccl_hip_key_kind key, uint32_t arity) {
   if (arity == 1) {
     if (key_bytes(key) == 0) return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "search key kind");
   } else if (key != RCCL_HIP_KEY_U32 || arity < 2 || arity > 6) {
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "search key kind or arity");
   }
+  return ok();
+}
+
+} // namespace
+
+extern "C" {
+
+rccl_hip_status rccl_hip_bound_search_workspace_bytes(rccl_hip_key_kind key, uint32_t arity,
+                                                      size_t n, size_t *bytes) {
+  if (!bytes) return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "bytes");
+  RCCL_HIP_TRY(check_key(key, arity));
+  *bytes = index_bytes(key, arity, n);
+  return ok();
+}
+
+
+rccl_hip_status rccl_hip_bound_search(rccl_hip_key_kind key, uint32_t arity, rccl_hip_order order,
+                                      int upper, const void *haystack, size_t n,
+                                      const void *needles, size_t m, uint64_t *out_indices,
+                                      void *workspace, size_t workspace_bytes,
+                                      hipStream_t stream) {
+  RCCL_HIP_TRY(check_key(key, arity));
   if (order != RCCL_HIP_ORDER_ASCENDING && order != RCCL_HIP_ORDER_DESCENDING)
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "order");
   if (arity > 1 && order != RCCL_HIP_ORDER_ASCENDING)
@@ -58,7 +99,8 @@ rccl_hip_status rccl_hip_bound_search(rccl_hip_key_kind key, uint32_t arity, rcc
   if (m && (!needles || !out_indices))
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "search needles or output");
   if (m && n && !haystack) return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "search haystack");
-  const search::SearchArgs a{haystack, needles, n, m, out_indices, upper != 0, stream};
+  const search::SearchArgs a{haystack, needles, n,         m, out_indices, upper != 0,
+                            workspace, workspace_bytes, stream};
   return dispatch(key, arity, order == RCCL_HIP_ORDER_DESCENDING, a);
 }
 

@@ -8,12 +8,22 @@
 // reverse, or the lexicographic order of [u32; N] rows.
 //
 // Design: one thread per needle, blocks striding over the needles. Every
-// block first copies a sample of the haystack into LDS, element
-// (s + 1) * step - 1 for s < SAMPLES with step = ceil(n / SAMPLES): the
-// boundaries of an implicit search tree's top levels. A thread searches the sample in LDS, which brackets its answer in
-// one step-long span, then finishes with a binary search over that span in
-// global memory: ceil(log2(step)) dependent global loads instead of
-// ceil(log2(n)).
+// block first copies a sample of the searched array into LDS, element
+// (s + 1) * step - 1 for s < SAMPLES with step = ceil(len / SAMPLES): the
+// boundaries of an implicit search tree's top levels. A thread searches the
+// sample in LDS, which brackets its answer in one step-long span, then
+// finishes with a binary search over that span in global memory.
+//
+// Large haystacks with many needles are searched through a two-level index
+// built per call, a B+-tree over cache lines: index[c] is the last item of
+// the haystack's c-th 128-byte chunk (CHUNK items), and lines[j] the last
+// item of its j-th run of CHUNK chunks (the last entry of index line j). The
+// sampled search above runs over `lines` (a CHUNK^2-th of the haystack, hot
+// in L2) and yields the first index line whose last entry is not before x;
+// a search inside that index line gives the chunk, and one inside the chunk
+// the answer: one cache line of each level. Searching the haystack directly
+// costs a cache line per level below the LDS sample (about ten at 2^26
+// items), and random needles share almost none of them.
 #pragma once
 
 #include <type_traits>
@@ -32,6 +42,12 @@ constexpr uint32_t samples_for() {
   return static_cast<uint32_t>(16384 / sizeof(K));
 }
 
+// Haystack items per index entry: one 128-byte cache line's worth.
+template <class K>
+constexpr size_t chunk_items() {
+  return sizeof(K) >= 128 ? 1 : 128 / sizeof(K);
+}
+
 // Predicate "item i belongs before the answer": h < x for lower_bound,
 // !(x < h) for upper_bound. True on a prefix of a sorted haystack.
 template <class K, class Cmp, bool UPPER>
@@ -43,38 +59,99 @@ struct Before {
   }
 };
 
-template <class K, class Cmp, bool UPPER, uint32_t SAMPLES>
+// index[c] = hay[min((c + 1) * CHUNK, n) - 1] for c < chunks, and
+// lines[j] = index[min((j + 1) * CHUNK, chunks) - 1] for j < ceil(chunks /
+// CHUNK), written by the thread of that index entry.
+template <class K>
 __global__ void __launch_bounds__(THREADS)
-search_kernel(const K *__restrict__ hay, size_t n, const K *__restrict__ needles, size_t m,
-              uint64_t *__restrict__ out, size_t step) {
+index_kernel(const K *__restrict__ hay, size_t n, K *__restrict__ index, size_t chunks,
+             K *__restrict__ lines) {
+  constexpr size_t CHUNK = chunk_items<K>();
+  for (size_t c = size_t(blockIdx.x) * THREADS + threadIdx.x; c < chunks;
+       c += size_t(gridDim.x) * THREADS) {
+    const K v = hay[std::min((c + 1) * CHUNK, n) - 1];
+    index[c] = v;
+    if ((c + 1) % CHUNK == 0 || c + 1 == chunks) lines[c / CHUNK] = v;
+  }
+}
+
+// First position in [a, b] whose item is not before x, given that arr[b] is
+// not before x (a sorted run inside one cache line).
+template <class K, class B>
+__device__ __forceinline__ size_t first_in_line(const K *__restrict__ arr, size_t a, size_t b,
+                                                const K &x, B before) {
+  while (a < b) {
+    const size_t mid = a + (b - a) / 2;
+    if (before(arr[mid], x)) a = mid + 1;
+    else b = mid;
+  }
+  return a;
+}
+
+// First position p < len with !before(arr[p], x), or len: the LDS sample
+// (sample[s] = arr[(s + 1) * step - 1], s < used) brackets p in one span,
+// searched in global memory.
+template <class K, class B, uint32_t SAMPLES>
+__device__ __forceinline__ size_t first_not_before(const K *__restrict__ arr, size_t len,
+                                                   const K *sample, uint32_t used, size_t step,
+                                                   const K &x, B before) {
+  uint32_t lo = 0, hi = used;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (before(sample[mid], x)) lo = mid + 1;
+    else hi = mid;
+  }
+  // Items [lo * step, (lo + 1) * step - 1) remain (to len past the last
+  // sample); the item at (lo + 1) * step - 1, sample lo, is not before x.
+  size_t a = size_t(lo) * step;
+  size_t b = lo < used ? (size_t(lo) + 1) * step - 1 : len;
+  while (a < b) {
+    const size_t mid = a + (b - a) / 2;
+    if (before(arr[mid], x)) a = mid + 1;
+    else b = mid;
+  }
+  return a;
+}
+
+// INDEXED: the sampled search runs over the index lines and finishes with
+// one line of the index and one chunk of the haystack; otherwise it runs
+// over the haystack itself.
+template <class K, class Cmp, bool UPPER, uint32_t SAMPLES, bool INDEXED>
+__global__ void __launch_bounds__(THREADS)
+search_kernel(const K *__restrict__ hay, size_t n, const K *__restrict__ index, size_t chunks,
+              const K *__restrict__ lines, size_t nlines, const K *__restrict__ needles,
+              size_t m, uint64_t *__restrict__ out, size_t step) {
   __shared__ K sample[SAMPLES];
+  constexpr size_t CHUNK = chunk_items<K>();
   const Before<K, Cmp, UPPER> before{};
-  // Sample s is hay[(s + 1) * step - 1]; samples past the end are unused.
-  const uint32_t used = static_cast<uint32_t>(std::min<size_t>(SAMPLES, n / step));
+  const K *arr = INDEXED ? lines : hay;
+  const size_t len = INDEXED ? nlines : n;
+  // Sample s is arr[(s + 1) * step - 1]; samples past the end are unused.
+  const uint32_t used = static_cast<uint32_t>(std::min<size_t>(SAMPLES, len / step));
   for (uint32_t s = threadIdx.x; s < used; s += THREADS)
-    sample[s] = hay[(size_t(s) + 1) * step - 1];
+    sample[s] = arr[(size_t(s) + 1) * step - 1];
   __syncthreads();
   // Blocks stride over the needles, so the sample is loaded once per block.
   for (size_t q = size_t(blockIdx.x) * THREADS + threadIdx.x; q < m;
        q += size_t(gridDim.x) * THREADS) {
     const K x = needles[q];
-    // First sample not before x.
-    uint32_t lo = 0, hi = used;
-    while (lo < hi) {
-      const uint32_t mid = (lo + hi) >> 1;
-      if (before(sample[mid], x)) lo = mid + 1;
-      else hi = mid;
+    size_t p = first_not_before<K, Before<K, Cmp, UPPER>, SAMPLES>(arr, len, sample, used, step,
+                                                                   x, before);
+    if constexpr (INDEXED) {
+      // Every index line before j ends with an entry before x, so all of its
+      // chunks end before x and so do all their items; line j's last entry
+      // is not. Likewise inside the line for the chunk, and inside the chunk
+      // for the answer; n when no line qualifies.
+      const size_t j = p;
+      if (j == nlines) {
+        p = n;
+      } else {
+        const size_t c = first_in_line(index, j * CHUNK, std::min((j + 1) * CHUNK, chunks) - 1,
+                                       x, before);
+        p = first_in_line(hay, c * CHUNK, std::min((c + 1) * CHUNK, n) - 1, x, before);
+      }
     }
-    // Items [lo * step, (lo + 1) * step - 1) remain (to n past the last
-    // sample); the item at (lo + 1) * step - 1, sample lo, is not before x.
-    size_t a = size_t(lo) * step;
-    size_t b = lo < used ? (size_t(lo) + 1) * step - 1 : n;
-    while (a < b) {
-      const size_t mid = a + (b - a) / 2;
-      if (before(hay[mid], x)) a = mid + 1;
-      else b = mid;
-    }
-    out[q] = a;
+    out[q] = p;
   }
 }
 
@@ -83,6 +160,8 @@ struct SearchArgs {
   size_t n, m;
   uint64_t *out;
   bool upper;
+  void *ws;
+  size_t ws_bytes;
   hipStream_t stream;
 };
 
@@ -90,11 +169,42 @@ struct SearchArgs {
 // global loads' latency).
 constexpr size_t BLOCKS_PER_CU = 8;
 
+// The index pays when the haystack is larger than the LDS sample can bracket
+// to one chunk, and there are enough needles to repay reading the haystack
+// once to build it (each indexed needle saves several cache lines).
+template <class K>
+size_t index_chunks(size_t n) {
+  const size_t chunks = (n + chunk_items<K>() - 1) / chunk_items<K>();
+  return chunks > samples_for<K>() ? chunks : 0;
+}
+template <class K>
+size_t index_lines(size_t chunks) {
+  return (chunks + chunk_items<K>() - 1) / chunk_items<K>();
+}
+template <class K>
+size_t workspace_bytes(size_t n) {
+  const size_t chunks = index_chunks<K>(n);
+  if (chunks == 0) return 0;
+  return align_up(chunks * sizeof(K), 256) + align_up(index_lines<K>(chunks) * sizeof(K), 256);
+}
+template <class K>
+bool use_index(size_t n, size_t m) {
+  const size_t chunks = index_chunks<K>(n);
+  return chunks && m >= chunks / 4;
+}
+
 template <class K, class Cmp>
 rccl_hip_status run(const SearchArgs &a) {
   if (a.m == 0) return ok();
   constexpr uint32_t SAMPLES = samples_for<K>();
-  const size_t step = std::max<size_t>(1, (a.n + SAMPLES - 1) / SAMPLES);
+  const bool indexed = use_index<K>(a.n, a.m);
+  const size_t chunks = indexed ? index_chunks<K>(a.n) : 0;
+  if (indexed && (!a.ws || a.ws_bytes < workspace_bytes<K>(a.n)))
+    return set_error(RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL, "search workspace",
+                     workspace_bytes<K>(a.n), a.ws_bytes);
+  const size_t nlines = indexed ? index_lines<K>(chunks) : 0;
+  const size_t len = indexed ? nlines : a.n;
+  const size_t step = std::max<size_t>(1, (len + SAMPLES - 1) / SAMPLES);
   static int cus = 0;
   if (cus == 0) {
     int dev = 0;
@@ -103,15 +213,37 @@ rccl_hip_status run(const SearchArgs &a) {
       err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "search device", err);
   }
+  const K *hay = static_cast<const K *>(a.hay);
+  K *index = static_cast<K *>(a.ws);
+  K *lines = indexed ? reinterpret_cast<K *>(static_cast<unsigned char *>(a.ws) +
+                                             align_up(chunks * sizeof(K), 256))
+                     : nullptr;
+  if (indexed) {
+    KernelTimer t("search_index", a.stream, chunks);
+    const dim3 grid(static_cast<uint32_t>(
+        std::min<size_t>((chunks + THREADS - 1) / THREADS, size_t(cus) * BLOCKS_PER_CU)));
+    index_kernel<K><<<grid, THREADS, 0, a.stream>>>(hay, a.n, index, chunks, lines);
+    RCCL_HIP_TRY(check_launch("search index"));
+  }
   const dim3 grid(static_cast<uint32_t>(
       std::min<size_t>((a.m + THREADS - 1) / THREADS, size_t(cus) * BLOCKS_PER_CU)));
   KernelTimer t("search", a.stream, a.m);
-  if (a.upper)
-    search_kernel<K, Cmp, true, SAMPLES><<<grid, THREADS, 0, a.stream>>>(
-        static_cast<const K *>(a.hay), a.n, static_cast<const K *>(a.needles), a.m, a.out, step);
-  else
-    search_kernel<K, Cmp, false, SAMPLES><<<grid, THREADS, 0, a.stream>>>(
-        static_cast<const K *>(a.hay), a.n, static_cast<const K *>(a.needles), a.m, a.out, step);
+  const K *needles = static_cast<const K *>(a.needles);
+  if (indexed) {
+    if (a.upper)
+      search_kernel<K, Cmp, true, SAMPLES, true><<<grid, THREADS, 0, a.stream>>>(
+          hay, a.n, index, chunks, lines, nlines, needles, a.m, a.out, step);
+    else
+      search_kernel<K, Cmp, false, SAMPLES, true><<<grid, THREADS, 0, a.stream>>>(
+          hay, a.n, index, chunks, lines, nlines, needles, a.m, a.out, step);
+  } else {
+    if (a.upper)
+      search_kernel<K, Cmp, true, SAMPLES, false><<<grid, THREADS, 0, a.stream>>>(
+          hay, a.n, nullptr, 0, nullptr, 0, needles, a.m, a.out, step);
+    else
+      search_kernel<K, Cmp, false, SAMPLES, false><<<grid, THREADS, 0, a.stream>>>(
+          hay, a.n, nullptr, 0, nullptr, 0, needles, a.m, a.out, step);
+  }
   return check_launch("search");
 }
 

@@ -488,9 +488,11 @@ def _bound(execution, haystack, needles, output, order, upper):
     if out.dtype != np.dtype(np.uint64):
         raise TypeError("bound indices are u64")
     _capacity("bound-search output", q.len(), out.len())
+    nbytes = _abi.workspace_bytes("rccl_hip_bound_search_workspace_bytes", kind, arity, h.len())
+    ws = DeviceBuffer.bytes(nbytes, execution.launch().program.device)
     _abi.check(_abi.load().rccl_hip_bound_search(
         kind, arity, cub.order_code(order), int(upper), h.ptr, h.len(), q.ptr, q.len(), out.ptr,
-        execution.launch().handle))
+        ws.ptr, nbytes, execution.launch().handle))
     execution.synchronize()
 
 

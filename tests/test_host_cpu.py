@@ -334,3 +334,40 @@ def test_device_generators_match_host_on_cpu():
     assert _same_bits(wd.c4_merge_sort_keys(n, "cpu"), workloads.c4_merge_sort_keys(n))
     for d, h in zip(wd.c5_inputs(n, "cpu"), workloads.c5_inputs(n)):
         assert _same_bits(d, h)
+
+
+def test_bound_search_workspace_and_validation(lib):
+    """The bound search's two-level index: one item per 128-byte haystack chunk
+    and one per 128-byte line of those, none while the LDS sample already
+    brackets every needle in one chunk; a call that builds it fails before
+    any launch when the workspace is short."""
+    ws = lambda key, arity, n: _abi.workspace_bytes(  # noqa: E731
+        "rccl_hip_bound_search_workspace_bytes", key, arity, n)
+
+    def align(x):
+        return (x + 255) // 256 * 256
+
+    def expect(n, item):
+        chunk = max(1, 128 // item)
+        chunks = -(-n // chunk)
+        if chunks <= 16384 // item:  # the LDS sample's size
+            return 0
+        return align(chunks * item) + align(-(-chunks // chunk) * item)
+    assert ws(0, 1, 4096 * 32) == 0            # u32: 4,096 samples x 32 per chunk
+    assert ws(0, 1, 4096 * 32 + 1) == align(4097 * 4) + align(129 * 4)
+    assert ws(0, 1, 1 << 26) == (1 << 21) * 4 + (1 << 16) * 4  # the benchmark haystack
+    assert ws(6, 1, 16384 * 128) == 0          # u8: 16,384 samples x 128 per chunk
+    for key, item in [(0, 4), (3, 8), (6, 1), (8, 2), (5, 8)]:
+        for n in (1000, 1 << 20, (1 << 26) + 3):
+            assert ws(key, 1, n) == expect(n, item), (key, n)
+    for arity in range(2, 7):
+        assert ws(0, arity, 10_000_000) == expect(10_000_000, 4 * arity), arity
+    out = ctypes.c_size_t(0)
+    assert lib.rccl_hip_bound_search_workspace_bytes(0, 7, 10, ctypes.byref(out)) == 9
+    assert lib.rccl_hip_bound_search_workspace_bytes(42, 1, 10, ctypes.byref(out)) == 9
+    n, m = 1 << 26, 1 << 20
+    need = ws(0, 1, n)
+    assert lib.rccl_hip_bound_search(0, 1, 0, 0, FAKE, n, FAKE, m, FAKE, FAKE, need - 1,
+                                     None) == 2
+    assert lib.rccl_hip_bound_search(0, 1, 0, 0, FAKE, n, FAKE, m, FAKE, None, 0, None) == 2
+    assert lib.rccl_hip_bound_search(0, 1, 0, 0, FAKE, n, FAKE, 0, FAKE, None, 0, None) == 0

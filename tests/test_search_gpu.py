@@ -114,3 +114,22 @@ def test_output_capacity(ex):
     q = DeviceBuffer.from_host(np.arange(5, dtype=np.uint32))
     with pytest.raises(thrust.DeviceAlgorithmError, match="bound-search output"):
         thrust.lower_bound(ex, hay, q, DeviceBuffer.zeroed(np.uint64, 4))
+
+
+@pytest.mark.parametrize("kind", ["u8", "i16", "u32", "f64"])
+def test_index_and_direct_paths(ex, kind):
+    """A large haystack: many needles search through the per-call chunk index,
+    a few search the haystack directly; both agree with searchsorted, for
+    needles drawn from the values, haystack items at and around chunk
+    boundaries (every chunk is 128 bytes), and the extremes."""
+    n = (1 << 22) + 5
+    distinct = 256 if kind == "u8" else 1 << 20
+    hay = np.sort(_values(kind, n, 31, distinct))
+    chunk = 128 // hay.dtype.itemsize
+    edges = np.arange(chunk - 1, n, chunk * 97)
+    for m in (300_001, 1_000):
+        needles = np.concatenate([hay[[0, n - 1]], hay[edges], hay[np.minimum(edges + 1, n - 1)],
+                                  _values(kind, m, 32, distinct + 7)])[:m]
+        assert np.array_equal(_search(ex, hay, needles), np.searchsorted(hay, needles, "left"))
+        assert np.array_equal(_search(ex, hay, needles, upper=True),
+                              np.searchsorted(hay, needles, "right"))
