@@ -113,14 +113,46 @@ __device__ __forceinline__ size_t first_not_before(const K *__restrict__ arr, si
   return a;
 }
 
+// Items searched a whole line at a time: 4 to 16 bytes that tile 128 bytes
+// (narrower ones would need a register per item to compare).
+template <class K>
+constexpr bool line_items() {
+  return sizeof(K) >= 4 && 128 % sizeof(K) == 0;
+}
+
+// Number of the first `valid` items of a 16-byte-aligned 128-byte line that
+// are before x: the line is read whole with eight independent 16-byte loads
+// and compared in registers, one memory round trip where a binary search
+// inside the line chains five.
+template <class K, class B>
+__device__ __forceinline__ uint32_t count_before(const K *__restrict__ line, uint32_t valid,
+                                                 const K &x, B before) {
+  static_assert(128 % sizeof(K) == 0, "whole items per line");
+  constexpr int ITEMS = 128 / sizeof(K);
+  uint4 raw[8];
+  const uint4 *p = reinterpret_cast<const uint4 *>(line);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) raw[i] = p[i];
+  K v[ITEMS];
+  __builtin_memcpy(v, raw, 128);
+  uint32_t cnt = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) cnt += (uint32_t(i) < valid && before(v[i], x)) ? 1u : 0u;
+  return cnt;
+}
+
 // INDEXED: the sampled search runs over the index lines and finishes with
 // one line of the index and one chunk of the haystack; otherwise it runs
-// over the haystack itself.
-template <class K, class Cmp, bool UPPER, uint32_t SAMPLES, bool INDEXED>
+// over the haystack itself. LINES (indexed, items dividing 128 bytes, at
+// most SAMPLES lines of `lines`): the sample holds the last entry of every
+// 128-byte line of `lines` (step == CHUNK), and each level below is one
+// line read whole (count_before); the haystack chunk too when the haystack
+// is 16-byte aligned (hay16) and the chunk full.
+template <class K, class Cmp, bool UPPER, uint32_t SAMPLES, bool INDEXED, bool LINES>
 __global__ void __launch_bounds__(THREADS)
 search_kernel(const K *__restrict__ hay, size_t n, const K *__restrict__ index, size_t chunks,
               const K *__restrict__ lines, size_t nlines, const K *__restrict__ needles,
-              size_t m, uint64_t *__restrict__ out, size_t step) {
+              size_t m, uint64_t *__restrict__ out, size_t step, bool hay16) {
   __shared__ K sample[SAMPLES];
   constexpr size_t CHUNK = chunk_items<K>();
   const Before<K, Cmp, UPPER> before{};
@@ -135,6 +167,37 @@ search_kernel(const K *__restrict__ hay, size_t n, const K *__restrict__ index, 
   for (size_t q = size_t(blockIdx.x) * THREADS + threadIdx.x; q < m;
        q += size_t(gridDim.x) * THREADS) {
     const K x = needles[q];
+    if constexpr (LINES && line_items<K>()) {
+      // Line L of `lines`: the first whose last entry is not before x (the
+      // sample holds the full lines' last entries; L == used is the partial
+      // last line, or past the end).
+      uint32_t lo = 0, hi = used;
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (before(sample[mid], x)) lo = mid + 1;
+        else hi = mid;
+      }
+      size_t p = n;
+      const size_t l0 = size_t(lo) * CHUNK;
+      if (l0 < nlines) {
+        const size_t j = l0 + count_before(lines + l0, uint32_t(std::min(CHUNK, nlines - l0)), x,
+                                           before);
+        if (j < nlines) {
+          const size_t i0 = j * CHUNK;
+          // Below chunks for a sorted haystack; clamped so that an unsorted
+          // one (unspecified results) still reads in bounds.
+          const size_t c = std::min(
+              chunks - 1,
+              i0 + count_before(index + i0, uint32_t(std::min(CHUNK, chunks - i0)), x, before));
+          const size_t h0 = c * CHUNK;
+          p = hay16 && h0 + CHUNK <= n
+                  ? h0 + count_before(hay + h0, uint32_t(CHUNK), x, before)
+                  : first_in_line(hay, h0, std::min(h0 + CHUNK, n) - 1, x, before);
+        }
+      }
+      out[q] = p;
+      continue;
+    }
     size_t p = first_not_before<K, Before<K, Cmp, UPPER>, SAMPLES>(arr, len, sample, used, step,
                                                                    x, before);
     if constexpr (INDEXED) {
@@ -204,7 +267,12 @@ rccl_hip_status run(const SearchArgs &a) {
                      workspace_bytes<K>(a.n), a.ws_bytes);
   const size_t nlines = indexed ? index_lines<K>(chunks) : 0;
   const size_t len = indexed ? nlines : a.n;
-  const size_t step = std::max<size_t>(1, (len + SAMPLES - 1) / SAMPLES);
+  constexpr size_t CHUNK = chunk_items<K>();
+  const bool line_search =
+      indexed && line_items<K>() && (nlines + CHUNK - 1) / CHUNK <= SAMPLES;
+  const size_t step =
+      line_search ? CHUNK : std::max<size_t>(1, (len + SAMPLES - 1) / SAMPLES);
+  const bool hay16 = reinterpret_cast<uintptr_t>(a.hay) % 16 == 0;
   static int cus = 0;
   if (cus == 0) {
     int dev = 0;
@@ -229,20 +297,24 @@ rccl_hip_status run(const SearchArgs &a) {
       std::min<size_t>((a.m + THREADS - 1) / THREADS, size_t(cus) * BLOCKS_PER_CU)));
   KernelTimer t("search", a.stream, a.m);
   const K *needles = static_cast<const K *>(a.needles);
-  if (indexed) {
-    if (a.upper)
-      search_kernel<K, Cmp, true, SAMPLES, true><<<grid, THREADS, 0, a.stream>>>(
-          hay, a.n, index, chunks, lines, nlines, needles, a.m, a.out, step);
-    else
-      search_kernel<K, Cmp, false, SAMPLES, true><<<grid, THREADS, 0, a.stream>>>(
-          hay, a.n, index, chunks, lines, nlines, needles, a.m, a.out, step);
+  auto launch = [&](auto upper, auto idx, auto lines_mode) {
+    search_kernel<K, Cmp, decltype(upper)::value, SAMPLES, decltype(idx)::value,
+                  decltype(lines_mode)::value><<<grid, THREADS, 0, a.stream>>>(
+        hay, a.n, index, chunks, lines, nlines, needles, a.m, a.out, step, hay16);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  if (line_search) {
+    if constexpr (line_items<K>()) {
+      if (a.upper) launch(T{}, T{}, T{});
+      else launch(F{}, T{}, T{});
+    }
+  } else if (indexed) {
+    if (a.upper) launch(T{}, T{}, F{});
+    else launch(F{}, T{}, F{});
   } else {
-    if (a.upper)
-      search_kernel<K, Cmp, true, SAMPLES, false><<<grid, THREADS, 0, a.stream>>>(
-          hay, a.n, nullptr, 0, nullptr, 0, needles, a.m, a.out, step);
-    else
-      search_kernel<K, Cmp, false, SAMPLES, false><<<grid, THREADS, 0, a.stream>>>(
-          hay, a.n, nullptr, 0, nullptr, 0, needles, a.m, a.out, step);
+    if (a.upper) launch(T{}, F{}, F{});
+    else launch(F{}, F{}, F{});
   }
   return check_launch("search");
 }

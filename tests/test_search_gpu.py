@@ -133,3 +133,21 @@ def test_index_and_direct_paths(ex, kind):
         assert np.array_equal(_search(ex, hay, needles), np.searchsorted(hay, needles, "left"))
         assert np.array_equal(_search(ex, hay, needles, upper=True),
                               np.searchsorted(hay, needles, "right"))
+
+
+@pytest.mark.parametrize("kind", ["u32", "f64"])
+def test_unaligned_haystack(ex, kind):
+    """A haystack that starts one item past a 16-byte boundary: the index
+    levels are still read a line at a time, the haystack chunk by binary
+    search."""
+    n = (1 << 21) + 3
+    hay = np.sort(_values(kind, n, 41, 1 << 19))
+    padded = DeviceBuffer.from_host(np.concatenate([hay[:1], hay]))
+    h = DeviceBuffer(padded.tensor[1:], hay.dtype, n)
+    assert h.ptr % 16 != 0
+    needles = np.concatenate([hay[[0, n - 1]], _values(kind, 200_000, 42, (1 << 19) + 5)])
+    for upper, side in ((False, "left"), (True, "right")):
+        out = DeviceBuffer.from_host(np.full(len(needles), 2**64 - 1, dtype=np.uint64))
+        (thrust.upper_bound if upper else thrust.lower_bound)(
+            ex, h, DeviceBuffer.from_host(needles), out)
+        assert np.array_equal(out.to_host_vec(), np.searchsorted(hay, needles, side))
