@@ -276,7 +276,8 @@ def run_merge_sort(torch, np, cub, abi, DeviceBuffer, wd, log2n, steps, warmup):
     def step():
         cub.device_merge_sort_keys_copy(launch, src, ws, out)
 
-    ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, launch.stream(), steps, warmup, step)
+    ms, ms_min, wall, kms, launches, per_step = time_steps(torch, abi, launch.stream(), steps,
+                                                           warmup, step)
     ok = _nondecreasing(torch, out.tensor, 32)
     ok = ok and _fingerprint(torch, out.tensor) == _fingerprint(torch, keys_t)
     res = {
@@ -286,16 +287,25 @@ def run_merge_sort(torch, np, cub, abi, DeviceBuffer, wd, log2n, steps, warmup):
         "ms_per_step": round(ms, 4), "ms_per_step_wall": round(wall, 4),
     }
     if "radix_onesweep" in kms:
-        # Integer keys lower to the stable radix sort (same permutation).
-        passes = launches.get("radix_onesweep", 0)
-        key_bytes = 4 + 8 * passes
+        # Integer keys lower to the stable radix sort (same permutation), which
+        # skips the passes whose byte is the same in every key (the copy form
+        # runs at least one). Active passes are the bytes that vary.
+        k64 = keys_t.to(torch.int64) & 0xFFFFFFFF
+        active = [i for i in range(4)
+                  if bool(((k64 >> (8 * i)) & 0xFF).unique().numel() > 1)] or [3]
+        sweeps = [[k for name, k in st if name == "radix_onesweep"] for st in per_step]
+        active_ms = [sw[i] for sw in sweeps for i in active]
+        idle_ms = [sw[i] for sw in sweeps for i in range(len(sw)) if i not in active]
+        key_bytes = 4 + 8 * len(active)
         res.update({
-            "lowering": "stable LSD radix sort (integer keys, natural order)",
-            "radix_passes": passes,
-            "bytes_model": f"{key_bytes} B/key = 4 B (histogram) + 8 B per radix pass",
-            "roofline": roofline(8.0 * n, kms["radix_onesweep"],
-                                 "radix_onesweep (one pass: 4n read + 4n write)",
+            "lowering": "stable LSD radix sort (integer keys, natural order), constant bytes "
+                        "skipped",
+            "radix_passes": len(active), "passes": launches.get("radix_onesweep", 0),
+            "bytes_model": f"{key_bytes} B/key = 4 B (histogram) + 8 B per active radix pass",
+            "roofline": roofline(8.0 * n, sum(active_ms) / len(active_ms),
+                                 "radix_onesweep, active passes (one pass: 4n read + 4n write)",
                                  profiled_traffic("merge_sort_radix_onesweep", log2n + 2)),
+            "idle_pass_ms": round(sum(idle_ms) / max(len(idle_ms), 1), 4),
         })
     else:
         passes = launches.get("merge_sort_pass", 0)

@@ -143,16 +143,17 @@ size_t single_tile_items(size_t key_bytes_, size_t value_bytes) {
 
 size_t merge_sort_lowering_bytes(size_t key_bytes_, size_t value_bytes, size_t n) {
   return align_up(n * key_bytes_, 256) + align_up(n * value_bytes, 256) +
-         layout(key_bytes_, value_bytes, n).total;
+         layout(key_bytes_, value_bytes, n).total + plan_bytes();
 }
 
 // A stable LSD radix sort of integer keys under the natural order or its
 // reverse yields exactly the stable merge sort's permutation: digit order is
 // integer order, and equal keys keep their input order. The output buffers
 // are the first half of the double buffer and the workspace's scratch the
-// second; a copy form reads its input in the histogram and the first pass
-// only. Keys of 4 and 8 bytes take 4 and 8 passes, an even count, so the
-// result ends in the output buffers.
+// second; a copy form reads its input in the histogram and its first active
+// pass only. The sort is planned: passes whose byte is the same in every key
+// (a digit holding all n keys) are skipped, and the plan routes the active
+// ones so that the last writes the output.
 rccl_hip_status merge_sort_lowering(rccl_hip_key_kind key, size_t value_bytes, bool descending,
                                     const void *in_keys, const void *in_vals, void *out_keys,
                                     void *out_vals, size_t n, void *workspace,
@@ -181,9 +182,10 @@ rccl_hip_status merge_sort_lowering(rccl_hip_key_kind key, size_t value_bytes, b
     a.src_keys = in_keys;
     a.src_vals = value_bytes ? in_vals : nullptr;
   }
+  a.planned = true;
   return sort_buffer(key, value_bytes,
                      descending ? RCCL_HIP_ORDER_DESCENDING : RCCL_HIP_ORDER_ASCENDING, a,
-                     workspace_bytes - scratch);
+                     workspace_bytes - scratch - plan_bytes());
 }
 } // namespace radix
 } // namespace rccl_hip

@@ -282,17 +282,63 @@ histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__
   }
 }
 
+// Pass plan of a sort that skips trivial passes (one digit holds every key:
+// the pass would not move anything). Buffers: 0 the input, 1 the output,
+// 2 the scratch; lb is the look-back buffer of the pass (the active passes
+// alternate, starting with buffer 0, which the histogram zeroes).
+struct PassPlan {
+  uint32_t active, src, dst, lb;
+};
+
+// Thread-serial plan for P passes, `trivial` bit p set when pass p is
+// trivial. The active passes alternate between output and scratch so that
+// the last one writes the output; the first reads the input. In place (input
+// == output) the first must write the scratch, so the active count must be
+// even: a trivial pass is activated when it is odd (P is even, so one
+// exists). Otherwise at least one pass runs, a stable copy into the output.
+__device__ inline void assign_plan(int P, uint32_t trivial, uint32_t in_place,
+                                   PassPlan *__restrict__ plan) {
+  uint32_t act = ~trivial & ((P >= 32 ? 0u : (1u << P)) - 1u);
+  int k = __builtin_popcount(act);
+  if (in_place) {
+    if (k & 1) {
+      act |= trivial & (0u - trivial);  // the lowest trivial pass
+      ++k;
+    }
+  } else if (k == 0) {
+    act = 1u << (P - 1);
+    k = 1;
+  }
+  uint32_t j = 0, prev = 0;
+  for (int p = 0; p < P; ++p) {
+    PassPlan e{0u, 0u, 0u, 0u};
+    if (act & (1u << p)) {
+      const uint32_t dst = ((uint32_t(k) - 1u - j) & 1u) ? 2u : 1u;
+      e = PassPlan{1u, j == 0 ? 0u : prev, dst, j & 1u};
+      prev = dst;
+      ++j;
+    }
+    plan[p] = e;
+  }
+}
+
 // Turn every pass's digit counts into exclusive offsets (the first output
 // position of each digit), once, so the onesweep blocks read them instead of
-// each scanning the bins. One block of BINS threads. (Internal linkage, like
-// init_kernel.)
+// each scanning the bins. One block of BINS threads. With a plan, it also
+// marks the trivial passes (a digit counting all n keys) and writes the pass
+// plan. (Internal linkage, like init_kernel.)
 namespace {
-__global__ void __launch_bounds__(BINS) bins_scan_kernel(uint32_t *bins, uint32_t passes) {
+__global__ void __launch_bounds__(BINS)
+bins_scan_kernel(uint32_t *bins, uint32_t passes, uint32_t n, PassPlan *plan, uint32_t in_place) {
   __shared__ uint32_t s_wave[BINS / 64];
+  __shared__ uint32_t s_trivial;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
+  if (tid == 0) s_trivial = 0;
+  __syncthreads();
   for (uint32_t p = 0; p < passes; ++p) {
     const uint32_t c = bins[p * BINS + tid];
+    if (plan && c == n) atomicOr(&s_trivial, 1u << p);
     const uint32_t inc = wave_inclusive_sum(c, lane);
     if (lane == 63) s_wave[tid >> 6] = inc;
     __syncthreads();
@@ -301,6 +347,7 @@ __global__ void __launch_bounds__(BINS) bins_scan_kernel(uint32_t *bins, uint32_
     bins[p * BINS + tid] = excl;
     __syncthreads();
   }
+  if (plan && tid == 0) assign_plan(static_cast<int>(passes), s_trivial, in_place, plan);
 }
 } // namespace
 
@@ -711,6 +758,34 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
                                                       mask);
 }
 
+// Input, output and scratch buffers of a planned sort (PassPlan numbering).
+template <class Bits, class Val>
+struct PlanBuffers {
+  const Bits *in;
+  Bits *out, *scratch;
+  const Val *vin;
+  Val *vout, *vscratch;
+};
+
+// One pass of a planned sort: inactive passes return at once; active ones
+// read and write the buffers and look-back buffer the plan names.
+template <class Bits, class Val, class Ops, int ITEMS, class Desc, int THREADS>
+__global__ void __launch_bounds__(THREADS, RCCL_RADIX_WAVES_PER_SIMD)
+planned_onesweep_kernel(PlanBuffers<Bits, Val> b, size_t n, uint32_t num_tiles,
+                        const uint32_t *__restrict__ pass_bins, const PassPlan *__restrict__ plan,
+                        LookbackBuf<Desc> lb0, LookbackBuf<Desc> lb1, uint32_t bit,
+                        uint32_t mask) {
+  const PassPlan pl = *plan;
+  if (!pl.active) return;
+  const Bits *kin = pl.src == 0 ? b.in : (pl.src == 1 ? b.out : b.scratch);
+  Bits *kout = pl.dst == 1 ? b.out : b.scratch;
+  const Val *vin = pl.src == 0 ? b.vin : (pl.src == 1 ? b.vout : b.vscratch);
+  Val *vout = pl.dst == 1 ? b.vout : b.vscratch;
+  onesweep_tile<Bits, Val, Ops, ITEMS, Desc, THREADS>(kin, kout, vin, vout, n, num_tiles,
+                                                      pass_bins, pl.lb ? lb1 : lb0,
+                                                      pl.lb ? lb0 : lb1, bit, mask);
+}
+
 // ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
@@ -744,7 +819,14 @@ struct SortArgs {
   // that must leave their input untouched start without a copy.
   const void *src_keys = nullptr;
   const void *src_vals = nullptr;
+  // Planned sorts skip trivial passes: keys[0] / vals[0] are the output,
+  // keys[1] / vals[1] the scratch, src_keys / src_vals the input (null: in
+  // place). The result always ends in the output. The plan needs
+  // plan_bytes() of workspace after the layout's.
+  bool planned = false;
 };
+
+inline size_t plan_bytes() { return align_up(8 * sizeof(PassPlan), 256); }
 
 template <class Bits, class Val, class Ops, class Desc>
 rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
@@ -789,9 +871,11 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
         reinterpret_cast<uint32_t *>(a.ws + l.lb[0]), zero_words);
   }
   RCCL_HIP_TRY(check_launch("radix histogram"));
+  PassPlan *plan = a.planned ? reinterpret_cast<PassPlan *>(a.ws + l.total) : nullptr;
   {
     KernelTimer t("radix_bins_scan", a.stream, passes * BINS);
-    bins_scan_kernel<<<1, BINS, 0, a.stream>>>(bins, passes);
+    bins_scan_kernel<<<1, BINS, 0, a.stream>>>(bins, passes, static_cast<uint32_t>(a.n), plan,
+                                                a.src_keys ? 0u : 1u);
   }
   RCCL_HIP_TRY(check_launch("radix bins scan"));
 
@@ -813,6 +897,25 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
     return set_error(RCCL_HIP_ERROR_LAUNCH, "radix onesweep does not fit on the device");
   const uint32_t grid = static_cast<uint32_t>(onesweep_grid(l.tiles));
 
+  if (a.planned) {
+    const PlanBuffers<Bits, Val> b{
+        static_cast<const Bits *>(a.src_keys ? a.src_keys : a.keys[0]),
+        static_cast<Bits *>(a.keys[0]), static_cast<Bits *>(a.keys[1]),
+        static_cast<const Val *>(a.src_keys ? a.src_vals : a.vals[0]),
+        static_cast<Val *>(a.vals[0]), static_cast<Val *>(a.vals[1])};
+    for (uint32_t p = 0; p < passes; ++p) {
+      const uint32_t bit = a.begin_bit + 8u * p;
+      const uint32_t mask = (1u << std::min(8u, a.end_bit - bit)) - 1u;
+      KernelTimer t("radix_onesweep", a.stream, a.n);
+      planned_onesweep_kernel<Bits, Val, Ops, ITEMS, Desc, THREADS>
+          <<<dim3(grid), THREADS, 0, a.stream>>>(b, a.n, static_cast<uint32_t>(l.tiles),
+                                                 bins + size_t(p) * BINS, plan + p, lb[0], lb[1],
+                                                 bit, mask);
+      RCCL_HIP_TRY(check_launch("radix onesweep"));
+    }
+    a.cur = 0;
+    return ok();
+  }
   for (uint32_t p = 0; p < passes; ++p) {
     const uint32_t bit = a.begin_bit + 8u * p;
     const uint32_t width = std::min(8u, a.end_bit - bit);

@@ -284,3 +284,33 @@ def test_merge_sort_c4_full_size(launch):
     keys = workloads.c4_merge_sort_keys(1 << 26)
     got = _merge_sort(launch, keys, copy=True)
     assert np.array_equal(got, np.sort(keys, kind="stable"))
+
+
+@pytest.mark.parametrize("kind", ["u32", "i64"])
+@pytest.mark.parametrize("shape", ["constant", "low_byte_constant", "top_byte_only"])
+def test_merge_sort_radix_lowering_trivial_passes(launch, kind, shape):
+    """The radix lowering skips passes whose byte is the same in every key;
+    the plan must still leave a stable result in the output, in place (even
+    active-pass count) and in the copy form (the input read first): every
+    key equal, the lowest byte constant, only the top byte varying."""
+    n = 200_003
+    dt = np.dtype(DTYPES[kind])
+    bits = 8 * dt.itemsize
+    raw = workloads.hash_range(77, n)
+    if shape == "constant":
+        keys = np.full(n, 7, dtype=dt)
+    elif shape == "low_byte_constant":
+        keys = ((raw >> np.uint64(72 - bits)) << np.uint64(8)).astype(dt.str.replace("i", "u")) \
+            .view(dt)
+    else:
+        keys = ((raw >> np.uint64(56)) << np.uint64(bits - 8)).astype(dt.str.replace("i", "u")) \
+            .view(dt)
+    vals = np.arange(n, dtype=np.uint32)
+    for descending in (False, True):
+        wk, wv = oracle.merge_sort(kind, keys, vals, descending)
+        for copy in (False, True):
+            gk, gv = _merge_sort(launch, keys, vals, descending, copy=copy)
+            assert np.array_equal(_bits(gk), _bits(wk)), (shape, descending, copy)
+            assert np.array_equal(gv, wv), (shape, descending, copy)
+        got = _merge_sort(launch, keys, descending=descending, copy=True)
+        assert np.array_equal(_bits(got), _bits(wk)), (shape, descending)
