@@ -33,9 +33,7 @@ using radix::BINS;
 using radix::LookbackBuf;
 
 // Source/destination buffers: 0 the input, 1 the output, 2 the scratch.
-struct PassPlan {
-  uint32_t active, src, dst, lb;
-};
+using radix::PassPlan;
 
 // Onesweep policy for rows: 512 threads x 4 rows = 2048-row tiles for every
 // arity (at most 48 KB of staged rows, two blocks per CU). At the reference
@@ -118,40 +116,9 @@ __device__ __forceinline__ void write_plan(uint32_t *__restrict__ bins, uint32_t
     bins[p * BINS + tid] = excl;
   }
   if (tid != 0) return;
-  bool act[P];
-  int k = 0;
-  for (int p = 0; p < P; ++p) {
-    act[p] = s_trivial[p] == 0;
-    k += act[p] ? 1 : 0;
-  }
-  if (in_place) {
-    // The last active pass writes the output, which is also the input: the
-    // first must read the input and write the scratch, so k must be even.
-    // k < P here (P is even), so a trivial pass exists.
-    if (k & 1) {
-      for (int p = 0; p < P; ++p) {
-        if (!act[p]) {
-          act[p] = true;
-          ++k;
-          break;
-        }
-      }
-    }
-  } else if (k == 0) {
-    act[P - 1] = true;  // a stable copy into the output
-    k = 1;
-  }
-  uint32_t j = 0, prev = 0;
-  for (int p = 0; p < P; ++p) {
-    PassPlan e{0u, 0u, 0u, 0u};
-    if (act[p]) {
-      const uint32_t dst = ((uint32_t(k) - 1u - j) & 1u) ? 2u : 1u;
-      e = PassPlan{1u, j == 0 ? 0u : prev, dst, j & 1u};
-      prev = dst;
-      ++j;
-    }
-    plan[p] = e;
-  }
+  uint32_t trivial = 0;
+  for (int p = 0; p < P; ++p) trivial |= s_trivial[p] ? (1u << p) : 0u;
+  radix::assign_plan(P, trivial, in_place, plan);
 }
 
 // Adds one wave's digits of byte `byte` of a column word to the LDS
