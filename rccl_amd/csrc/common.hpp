@@ -92,6 +92,26 @@ __device__ __forceinline__ T add_agent(T *p, T v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// gfx950 places the blocks of a launch on its 8 XCDs round-robin (block b on
+// XCD b % 8). xcd_order_tile(b) hands runs of RUN consecutive tiles to
+// consecutive blocks of one XCD, so neighbouring tiles share an L2. Within
+// one XCD, tile numbers rise with block numbers, and each XCD starts its
+// blocks in order. So in a decoupled look-back the lowest unfinished tile
+// has always been started (every earlier block of its XCD holds an earlier
+// tile, hence has finished), and the look-back cannot deadlock. The grid is
+// rounded up to whole rows of 8 * RUN blocks (xcd_order_grid); blocks whose
+// tile is past the end return.
+constexpr uint32_t XCDS = 8;
+template <uint32_t RUN>
+__device__ __forceinline__ uint32_t xcd_order_tile(uint32_t block) {
+  const uint32_t x = block % XCDS, j = block / XCDS;
+  return XCDS * RUN * (j / RUN) + RUN * x + j % RUN;
+}
+inline size_t xcd_order_grid(size_t tiles, uint32_t run) {
+  const size_t row = size_t(XCDS) * run;
+  return (tiles + row - 1) / row * row;
+}
+
 // Inclusive scan across the 64 lanes of a wave.
 template <class T>
 __device__ __forceinline__ T wave_inclusive_sum(T v, uint32_t lane) {

@@ -156,7 +156,6 @@ template <class Desc> struct LookbackBuf {
 constexpr int LOOKBACK = RCCL_RADIX_LOOKBACK_WINDOW;
 constexpr int GROUP = RCCL_RADIX_LOOKBACK_GROUP;
 constexpr int GWIN = RCCL_RADIX_GROUP_WINDOW;
-constexpr uint32_t XCDS = 8;  // gfx950: 8 XCDs, blocks placed round-robin
 constexpr uint32_t XCD_RUN = RCCL_RADIX_XCD_RUN;
 
 constexpr int threads_for(size_t value_bytes) {
@@ -384,22 +383,13 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Tile processed by a block. Blocks are placed on the XCDs round-robin
-// (block b on XCD b % 8), so giving runs of XCD_RUN consecutive tiles to
-// consecutive blocks of one XCD makes neighbouring tiles share an L2: the
-// cache lines they both write at digit-run boundaries are merged there
-// instead of reaching HBM as two partial writes. Every tile's predecessor
-// belongs to a block at most 8 * XCD_RUN - 9 indices later, far fewer than
-// the blocks resident at once, so in-order dispatch guarantees that the tile a
-// look-back waits on has been started.
+// Tile processed by a block, in XCD order (xcd_order_tile): the cache lines
+// that neighbouring tiles both write at digit-run boundaries are merged in
+// their shared L2 instead of reaching HBM as two partial writes.
 __device__ __forceinline__ uint32_t xcd_tile(uint32_t block) {
-  const uint32_t x = block % XCDS, j = block / XCDS;
-  return XCDS * XCD_RUN * (j / XCD_RUN) + XCD_RUN * x + j % XCD_RUN;
+  return xcd_order_tile<XCD_RUN>(block);
 }
-inline size_t onesweep_grid(size_t tiles) {
-  const size_t row = size_t(XCDS) * XCD_RUN;
-  return (tiles + row - 1) / row * row;
-}
+inline size_t onesweep_grid(size_t tiles) { return xcd_order_grid(tiles, XCD_RUN); }
 
 // Two-level decoupled look-back for one digit (one thread per digit): in-group
 // predecessors tile by tile until an inclusive prefix or the group start, then

@@ -312,7 +312,7 @@ rccl_hip_status run_radix(const RecordArgs &a) {
   }
   // The XCD-aware tile order needs the blocks of one row of runs (and the
   // next) resident at once.
-  if (size_t(blocks_per_cu) * size_t(cus) < 2 * size_t(radix::XCDS) * radix::XCD_RUN)
+  if (size_t(blocks_per_cu) * size_t(cus) < 2 * size_t(XCDS) * radix::XCD_RUN)
     return set_error(RCCL_HIP_ERROR_LAUNCH, "record radix onesweep does not fit on the device");
 
   {

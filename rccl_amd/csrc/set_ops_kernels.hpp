@@ -30,6 +30,7 @@ using ordering::NoValue;
 constexpr int THREADS = 512;
 constexpr int WAVES = THREADS / 64;
 constexpr size_t GROUP = lookback::GROUP;
+constexpr uint32_t XCD_RUN = 8;  // tiles per XCD run (xcd_order_tile)
 
 enum Op : int { UNION = 0, INTERSECTION = 1, DIFFERENCE = 2, SYMMETRIC_DIFFERENCE = 3 };
 
@@ -153,7 +154,6 @@ struct TileSmem {
   uint32_t split_b[THREADS + 1];
   uint32_t wave_total[WAVES];
   uint64_t tile_offset;
-  uint32_t tile;
 };
 
 // One serial step of operation OP on the current heads. Mirrors the four
@@ -202,7 +202,7 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
             const V *__restrict__ bv, const uint64_t *__restrict__ splits, size_t tiles,
             K *__restrict__ out, V *__restrict__ outv, size_t out_cap,
             uint64_t *__restrict__ out_count, uint64_t *desc, uint64_t *gagg, uint64_t *ginc,
-            uint32_t *ticket, Arith<K> ar, Arith<K> br) {
+            Arith<K> ar, Arith<K> br) {
   using Smem = TileSmem<K, V, ITEMS>;
   constexpr bool PAIRS = Smem::PAIRS;
   constexpr bool VALS_B = PAIRS && (OP == UNION || OP == SYMMETRIC_DIFFERENCE);
@@ -211,12 +211,11 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
-  // Tiles are numbered in the order blocks start (an atomic ticket), so every
-  // tile a look-back waits on has started earlier; block indices would not
-  // guarantee that, since the XCDs dispatch their blocks at their own pace.
-  if (tid == 0) sm.tile = add_agent(ticket, 1u);
-  __syncthreads();
-  const size_t t = sm.tile;
+  // Tiles in XCD order: every tile a look-back waits on has been started
+  // (xcd_order_tile), with no atomic ticket to take first, and neighbouring
+  // tiles share an L2.
+  const size_t t = xcd_order_tile<XCD_RUN>(blockIdx.x);
+  if (t >= tiles) return;
   const size_t i0 = splits[2 * t], j0 = splits[2 * t + 1];
   const size_t i1 = splits[2 * t + 2], j1 = splits[2 * t + 3];
   const uint32_t la = static_cast<uint32_t>(i1 - i0);
@@ -379,7 +378,7 @@ struct SetArgs {
 
 struct Layout {
   size_t tiles = 0, groups = 0;
-  size_t splits = 0, desc = 0, gagg = 0, ginc = 0, ticket = 0, total = 0;
+  size_t splits = 0, desc = 0, gagg = 0, ginc = 0, total = 0;
 };
 
 template <class K, class V>
@@ -398,8 +397,6 @@ Layout layout(size_t na, size_t nb) {
   off += l.groups * sizeof(uint64_t);
   l.ginc = off;
   off += l.groups * sizeof(uint64_t);
-  l.ticket = off;
-  off += sizeof(uint64_t);
   l.total = align_up(off, 256);
   return l;
 }
@@ -417,9 +414,8 @@ rccl_hip_status run_op(const SetArgs &s) {
   uint64_t *desc = reinterpret_cast<uint64_t *>(ws + l.desc);
   uint64_t *gagg = reinterpret_cast<uint64_t *>(ws + l.gagg);
   uint64_t *ginc = reinterpret_cast<uint64_t *>(ws + l.ginc);
-  uint32_t *ticket = reinterpret_cast<uint32_t *>(ws + l.ticket);
-  // Descriptors, group words and the ticket are contiguous.
-  const size_t state_words = l.tiles + 2 * l.groups + 1;
+  // Descriptors and group words are contiguous.
+  const size_t state_words = l.tiles + 2 * l.groups;
   {
     KernelTimer t("set_clear", s.stream, state_words);
     clear_kernel<<<dim3(static_cast<uint32_t>(std::min<size_t>((state_words + 255) / 256, 1024))),
@@ -427,7 +423,7 @@ rccl_hip_status run_op(const SetArgs &s) {
   }
   RCCL_HIP_TRY(check_launch("set clear"));
   const dim3 pgrid(static_cast<uint32_t>((l.tiles + 1 + 255) / 256));
-  const dim3 tgrid(static_cast<uint32_t>(l.tiles));
+  const dim3 tgrid(static_cast<uint32_t>(xcd_order_grid(l.tiles, XCD_RUN)));
   const K *a = static_cast<const K *>(s.a);
   const K *b = static_cast<const K *>(s.b);
   const V *av = static_cast<const V *>(s.av);
@@ -451,7 +447,7 @@ rccl_hip_status run_op(const SetArgs &s) {
         KernelTimer t("set_tile", s.stream, s.na + s.nb);
         tile_kernel<K, V, Cmp, OP, ITEMS, true><<<tgrid, THREADS, 0, s.stream>>>(
             a, av, b, bv, splits, l.tiles, out, outv, s.out_cap, s.out_count, desc, gagg, ginc,
-            ticket, ar, br);
+            ar, br);
       }
       return check_launch("set tile");
     } else {
@@ -469,7 +465,7 @@ rccl_hip_status run_op(const SetArgs &s) {
     KernelTimer t("set_tile", s.stream, s.na + s.nb);
     tile_kernel<K, V, Cmp, OP, ITEMS, false><<<tgrid, THREADS, 0, s.stream>>>(
         a, av, b, bv, splits, l.tiles, out, outv, s.out_cap, s.out_count, desc, gagg, ginc,
-        ticket, Arith<K>{}, Arith<K>{});
+        Arith<K>{}, Arith<K>{});
   }
   return check_launch("set tile");
 }

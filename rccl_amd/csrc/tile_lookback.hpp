@@ -1,6 +1,7 @@
 // Two-level decoupled look-back over per-tile counts, for kernels whose tiles
-// are numbered in start order (an atomic ticket) and that need each tile's
-// exclusive prefix: the set operations' and the compactions' output offsets.
+// are numbered so that every tile a look-back waits on has been started
+// (xcd_order_tile) and that need each tile's exclusive prefix: the set
+// operations' and the compactions' output offsets.
 //
 // Every tile publishes its count at once (flag AGG) and, after its look-back,
 // its inclusive prefix (flag INCL); it also adds (1 << GA_SHIFT) | count to
@@ -99,10 +100,10 @@ __device__ __forceinline__ uint64_t tile_prefix(size_t t, size_t tiles, uint64_t
 }
 
 // Words of look-back state for `tiles` tiles: descriptors, group aggregates
-// and group prefixes, plus one ticket word; all zeroed before a launch.
+// and group prefixes; all zeroed before a launch.
 inline size_t state_words(size_t tiles) {
   const size_t groups = (tiles + GROUP - 1) / GROUP;
-  return tiles + 2 * groups + 1;
+  return tiles + 2 * groups;
 }
 
 } // namespace lookback
