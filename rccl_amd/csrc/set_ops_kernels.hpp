@@ -27,17 +27,26 @@ namespace set_ops {
 
 using ordering::NoValue;
 
-constexpr int THREADS = 512;
+#ifndef RCCL_SET_THREADS
+#define RCCL_SET_THREADS 512
+#endif
+#ifndef RCCL_SET_ITEMS_8B
+#define RCCL_SET_ITEMS_8B 16
+#endif
+#ifndef RCCL_SET_XCD_RUN
+#define RCCL_SET_XCD_RUN 8
+#endif
+constexpr int THREADS = RCCL_SET_THREADS;
 constexpr int WAVES = THREADS / 64;
 constexpr size_t GROUP = lookback::GROUP;
-constexpr uint32_t XCD_RUN = 8;  // tiles per XCD run (xcd_order_tile)
+constexpr uint32_t XCD_RUN = RCCL_SET_XCD_RUN;  // tiles per XCD run (xcd_order_tile)
 
 enum Op : int { UNION = 0, INTERSECTION = 1, DIFFERENCE = 2, SYMMETRIC_DIFFERENCE = 3 };
 
 template <class K, class V>
 constexpr int items_for() {
   constexpr size_t bytes = sizeof(K) + (std::is_same<V, NoValue>::value ? 0 : sizeof(V));
-  return bytes <= 8 ? 16 : (bytes <= 16 ? 12 : 8);
+  return bytes <= 8 ? RCCL_SET_ITEMS_8B : (bytes <= 16 ? 12 : 8);
 }
 template <class K, class V>
 constexpr size_t tile_items() {
