@@ -8,7 +8,7 @@
  * declare these in an `extern "C"` block and keep the reference's public
  * surface (Program, Launch/Execution, views, typed workspaces) on top.
  *
- * Conventions (rccl-cub/src/error.rs:3-25, SURVEY of rccl-thrust/src/cuda.rs):
+ * Conventions (rccl-cub/src/error.rs:3-25, rccl-thrust/src/cuda.rs):
  *  - All pointers are device pointers unless stated otherwise; sizes are in
  *    elements. The caller owns inputs, outputs and the workspace; no entry
  *    point allocates device memory.
