@@ -10,8 +10,9 @@
  *
  * Conventions (rccl-cub/src/error.rs:3-25, rccl-thrust/src/cuda.rs):
  *  - All pointers are device pointers unless stated otherwise; sizes are in
- *    elements. The caller owns inputs, outputs and the workspace; no entry
- *    point allocates device memory.
+ *    elements. The caller owns inputs, outputs and the workspace; no
+ *    ordering entry point allocates device memory (only the one-time device
+ *    self-check of rccl_hip_program_load allocates and frees 4 bytes).
  *  - Work is enqueued on `stream` and is asynchronous (CUB semantics). The
  *    Thrust-style synchronous behaviour is the host layer's job.
  *  - Every call validates all arguments before the first launch and returns a
