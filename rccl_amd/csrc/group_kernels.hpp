@@ -92,6 +92,9 @@ struct IndependentProbabilityOr {  // f64: l + r - l * r, clamped to [0, 1]
   }
 };
 
+#ifndef RCCL_GROUP_ITEMS_8B
+#define RCCL_GROUP_ITEMS_8B 16
+#endif
 constexpr int THREADS = 256;
 constexpr uint32_t XCD_RUN = 8;  // tiles per XCD run (xcd_order_tile)
 constexpr int WAVES = THREADS / 64;
@@ -103,7 +106,7 @@ constexpr size_t bytes_of() {
 template <class K, class P, class V>
 constexpr int items_for() {
   constexpr size_t bytes = sizeof(K) + bytes_of<P>() + bytes_of<V>();
-  return bytes <= 8 ? 16 : (bytes <= 16 ? 12 : (bytes <= 32 ? 8 : 6));
+  return bytes <= 8 ? RCCL_GROUP_ITEMS_8B : (bytes <= 16 ? 12 : (bytes <= 32 ? 8 : 6));
 }
 template <class K, class P, class V>
 constexpr size_t tile_items() {
