@@ -61,10 +61,12 @@ def _buffer(torch, DeviceBuffer, t, np_dtype):
 
 def time_steps(torch, abi, stream, steps, warmup, step, before=None):
     """Run `step` warmup times, then `steps` timed times, then `steps` more
-    with the library's per-launch timing on. Returns (mean event ms, min, wall
-    ms, {kernel: mean ms}, {kernel: launches per step}, [[(kernel, ms), ...]
-    per profiled step]). The timed steps run without per-launch events, so
-    ``ms_per_step`` carries no timing overhead."""
+    with the library's per-launch timing on. Returns a dict: "ms" (median of
+    the per-step hipEvent times, the reference's protocol), "mean", "min",
+    "wall" (wall-clock ms per step, `before` included), "kernel_ms" ({kernel:
+    mean ms per launch}), "launches" ({kernel: launches per step}) and
+    "per_step" ([[(kernel, ms), ...] per profiled step]). The timed steps run
+    without per-launch events, so ``ms`` carries no timing overhead."""
     for _ in range(warmup):
         if before:
             before()
@@ -81,7 +83,7 @@ def time_steps(torch, abi, stream, steps, warmup, step, before=None):
         ends[k].record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    step_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    step_ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
     abi.timing_read()
     abi.timing_enable(True)
     per_step = []
@@ -96,9 +98,19 @@ def time_steps(torch, abi, stream, steps, warmup, step, before=None):
     for launches in per_step:
         for name, kms in launches:
             per.setdefault(name, []).append(kms)
-    return (sum(step_ms) / steps, min(step_ms), (t1 - t0) * 1e3 / steps,
-            {k: sum(v) / len(v) for k, v in per.items()},
-            {k: len(v) // steps for k, v in per.items()}, per_step)
+    mid = len(step_ms) // 2
+    median = step_ms[mid] if len(step_ms) % 2 else 0.5 * (step_ms[mid - 1] + step_ms[mid])
+    return {"ms": median, "mean": sum(step_ms) / steps, "min": step_ms[0],
+            "wall": (t1 - t0) * 1e3 / steps,
+            "kernel_ms": {k: sum(v) / len(v) for k, v in per.items()},
+            "launches": {k: len(v) // steps for k, v in per.items()}, "per_step": per_step}
+
+
+def _steps(*args, **kw):
+    """time_steps as (median ms, min ms, wall ms, kernel_ms, launches,
+    per_step)."""
+    t = time_steps(*args, **kw)
+    return t["ms"], t["min"], t["wall"], t["kernel_ms"], t["launches"], t["per_step"]
 
 
 def roofline(bytes_per_launch, launch_ms, kernel, traffic=None):
@@ -143,10 +155,52 @@ def _rounded(d):
 # ---------------------------------------------------------------------------
 # Radix sort legs (the metric).
 # ---------------------------------------------------------------------------
-def run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, values_t, steps, warmup):
+def _check_stable_pairs(torch, src_keys, out_keys, out_vals, bits):
+    """Exact check of a stable ascending sort of unsigned keys (same-width
+    signed tensors) whose values are their original indices: keys
+    non-decreasing, values a permutation, each value's key equal to its own
+    key in the input, and indices rising within every run of equal keys."""
+    n = src_keys.numel()
+    if not _nondecreasing(torch, out_keys, bits):
+        return False
+    idx = out_vals.to(torch.int64) & 0xFFFFFFFF
+    if not torch.equal(torch.sort(idx).values, torch.arange(n, device=idx.device)):
+        return False
+    if not torch.equal(src_keys[idx], out_keys):
+        return False
+    same = out_keys[1:] == out_keys[:-1]
+    return bool((idx[1:] > idx[:-1])[same].all().item())
+
+
+def _check_f32_descending(torch, src_bits, out_bits):
+    """Exact check of a descending f32 radix sort (int32 bit views): the same
+    multiset of bit patterns; positive NaNs first, then numbers non-increasing
+    under IEEE compare, then negative NaNs; the signed zeros in input order."""
+    if not torch.equal(torch.sort(out_bits).values, torch.sort(src_bits).values):
+        return False
+    out = out_bits.view(torch.float32)
+    nan = torch.isnan(out)
+    neg = out_bits < 0
+    pos_nan, neg_nan = int((nan & ~neg).sum()), int((nan & neg).sum())
+    n = out.numel()
+    if not bool(nan[:pos_nan].all()) or not bool(nan[n - neg_nan:].all()):
+        return False
+    mid = out[pos_nan:n - neg_nan]
+    if bool(torch.isnan(mid).any()) or not bool((mid[1:] <= mid[:-1]).all()):
+        return False
+    zo, zs = (out_bits & 0x7FFFFFFF) == 0, (src_bits & 0x7FFFFFFF) == 0
+    return bool(torch.equal(out_bits[zo], src_bits[zs]))
+
+
+def run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, values_t, steps, warmup, kdt=None,
+              descending=False):
+    """In-place radix sort of a device-resident input, restored from a
+    pristine copy before every step (outside the timed interval). Keys are
+    u32/u64 (or kdt), values u32 original indices or None."""
     n = keys_t.numel()
     launch = cub.Program.load(0).on(torch.cuda.current_stream(0))
-    kdt = np.uint32 if keys_t.dtype == torch.int32 else np.uint64
+    if kdt is None:
+        kdt = np.uint32 if keys_t.dtype == torch.int32 else np.uint64
     pristine_k = keys_t
     keys = _buffer(torch, DeviceBuffer, torch.empty_like(keys_t), kdt)
     if values_t is not None:
@@ -163,66 +217,124 @@ def run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, values_t, steps, warmup
 
     def sort():
         if values_t is not None:
-            cub.device_radix_sort_pairs(launch, keys, values, ws)
+            (cub.device_radix_sort_pairs_descending if descending
+             else cub.device_radix_sort_pairs)(launch, keys, values, ws)
         else:
-            cub.device_radix_sort_keys(launch, keys, ws)
+            (cub.device_radix_sort_keys_descending if descending
+             else cub.device_radix_sort_keys)(launch, keys, ws)
 
-    ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, launch.stream(), steps, warmup,
-                                                 sort, restore)
-    bits = 32 if kdt == np.uint32 else 64
-    ok = _nondecreasing(torch, keys.tensor, bits)
-    ok = ok and _fingerprint(torch, keys.tensor) == _fingerprint(torch, pristine_k)
-    if values_t is not None:
-        ok = ok and _fingerprint(torch, values.tensor) == _fingerprint(torch, pristine_v)
-    return {"n": n, "ms": ms, "ms_min": ms_min, "ms_wall": wall, "kernel_ms": kms,
-            "launches": launches, "validated": bool(ok)}
-
-
-def _rate(fn, keys, seconds):
-    """Gkeys/s of fn(keys) repeated for about `seconds` (at least once)."""
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        fn(keys)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            return reps * keys.size / el / 1e9, reps, el
+    t = time_steps(torch, abi, launch.stream(), steps, warmup, sort, restore)
+    bits = 8 * np.dtype(kdt).itemsize
+    if np.dtype(kdt) == np.float32 and descending and values_t is None:
+        ok = _check_f32_descending(torch, pristine_k, keys.tensor)
+    elif values_t is not None and not descending and np.dtype(kdt).kind == "u":
+        ok = _check_stable_pairs(torch, pristine_k, keys.tensor, values.tensor, bits)
+    else:
+        ok = _nondecreasing(torch, keys.tensor, bits) and \
+            _fingerprint(torch, keys.tensor) == _fingerprint(torch, pristine_k)
+    return {"n": n, "ms": t["ms"], "ms_mean": t["mean"], "ms_min": t["min"], "ms_wall": t["wall"],
+            "kernel_ms": t["kernel_ms"], "launches": t["launches"], "validated": bool(ok)}
 
 
-def cpu_baseline(keys_h, seconds, log2_sample):
-    """Host sorts of the first 2^log2_sample keys of the metric input, timed on
-    this machine's cores: the headline is a parallel comparison sort on every
-    core this process may use (at most 16, the GPU box's CPU share), the
-    substitute for the reference's rayon par_sort; beside it a single-thread
-    std::sort (slice::sort_unstable substitute) and the oracle's LSD radix
-    sort on 2^24 keys."""
-    import oracle
-
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    par, par_reps, par_el = _rate(lambda k: oracle.par_sort_unstable_u32(k, threads), keys_h,
-                                  seconds * 0.5)
-    small = keys_h[: 1 << min(24, log2_sample)]
-    one, one_reps, one_el = _rate(oracle.sort_unstable_u32, small, seconds * 0.3)
-    lsd, lsd_reps, lsd_el = _rate(lambda k: oracle.radix_sort("u32", k), small, seconds * 0.2)
+def radix_leg(r, n, workload, key_bytes_model, pass_bytes, kernel_desc, traffic_kernel, log2n,
+              dtype):
+    """One radix-sort bench leg: rate, the sort's bytes-model roofline and the
+    onesweep kernel's per-launch roofline."""
     return {
-        "value": round(par, 4),
-        "unit": "Gkeys/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"oracle/oracle_sort.cpp parallel sort (per-thread std::sort + merge-path "
-                  f"merges; substitute for rayon par_sort, no Rust toolchain here) over the "
-                  f"first 2^{log2_sample} keys of the benchmark input on {threads} threads, "
-                  f"{par_reps} sorts in {par_el:.1f} s",
-        "single_thread": {
-            "value": round(one, 4), "unit": "Gkeys/s", "cores": 1,
-            "sample": f"std::sort (slice::sort_unstable substitute) over the first "
-                      f"2^{small.size.bit_length() - 1} keys, {one_reps} sorts in {one_el:.1f} s"},
-        "lsd_radix_1core": {
-            "value": round(lsd, 4), "unit": "Gkeys/s", "cores": 1,
-            "sample": f"oracle/oracle.c stable LSD radix sort (8-bit passes) over the first "
-                      f"2^{small.size.bit_length() - 1} keys, {lsd_reps} sorts in {lsd_el:.1f} s"},
+        "workload": workload,
+        "value": round(n / (r["ms"] * 1e-3) / 1e9, 3), "unit": "Gkeys/s",
+        "ms_per_step": round(r["ms"], 4), "ms_per_step_mean": round(r["ms_mean"], 4),
+        "ms_per_step_min": round(r["ms_min"], 4), "ms_per_step_wall": round(r["ms_wall"], 4),
+        "dtype": dtype, "bytes_model": key_bytes_model[1],
+        "sort_roofline_frac": round(key_bytes_model[0] * n / (r["ms"] * 1e-3) / 1e9 /
+                                    HBM_PEAK_GBS, 4),
+        "roofline": roofline(pass_bytes * n, r["kernel_ms"]["radix_onesweep"], kernel_desc,
+                             profiled_traffic(traffic_kernel, log2n)),
+        "kernel_ms": _rounded(r["kernel_ms"]), "launches": r["launches"],
+        "validated": r["validated"],
     }
+
+
+def _median_rate(fn, items, reps=5):
+    """Median over `reps` runs of items / seconds of fn() (G items/s), and the
+    median seconds."""
+    secs = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        secs.append(time.perf_counter() - t0)
+    secs.sort()
+    med = secs[len(secs) // 2]
+    return items / med / 1e9, med
+
+
+def cpu_baseline(threads_cap=16):
+    """Host baselines on this machine's cores, each the median of 5 runs over
+    a bounded sample of the benchmark's own inputs (generation excluded).
+    They substitute for the reference's host validation oracles and rayon
+    (no Rust toolchain here): the headline is the parallel comparison sort of
+    u32 keys on every core this process may use (at most 16, the GPU box's
+    CPU share); beside it single-thread std::sort (slice::sort_unstable),
+    std::stable_sort of u64+u32 pairs (stable sort_by_key) single- and
+    multi-threaded, std::merge of u32 pairs (the reference's merge loop),
+    std::set_* over u64 multisets (host_set_by) and the oracle's LSD radix
+    sort."""
+    import numpy as np
+
+    import oracle
+    from rccl_amd import workloads
+
+    threads = max(1, min(threads_cap, len(os.sched_getaffinity(0))))
+    out = {}
+    keys26 = workloads.metric_u32_keys(1 << 26)
+    v, sec = _median_rate(lambda: oracle.par_sort_unstable_u32(keys26, threads), keys26.size)
+    head = {"value": round(v, 4), "unit": "Gkeys/s", "cores": threads, "kind": "port",
+            "sample": f"oracle/oracle_sort.cpp parallel sort (per-thread std::sort + merge-path "
+                      f"merges; substitute for rayon par_sort_unstable) of the first 2^26 keys of "
+                      f"the metric input on {threads} threads, median of 5 ({sec:.3f} s each)"}
+    keys22 = keys26[: 1 << 22]
+    v, sec = _median_rate(lambda: oracle.sort_unstable_u32(keys22), keys22.size)
+    out["u32_sort_unstable_1core"] = {
+        "value": round(v, 4), "unit": "Gkeys/s", "cores": 1,
+        "sample": f"std::sort (slice::sort_unstable substitute), first 2^22 metric keys, "
+                  f"median of 5 ({sec:.3f} s)"}
+    v, sec = _median_rate(lambda: oracle.radix_sort("u32", keys22), keys22.size)
+    out["u32_lsd_radix_1core"] = {
+        "value": round(v, 4), "unit": "Gkeys/s", "cores": 1,
+        "sample": f"oracle/oracle.c stable LSD radix sort (8-bit passes), first 2^22 metric "
+                  f"keys, median of 5 ({sec:.3f} s)"}
+    del keys26
+    pk, pv = workloads.metric_pairs(1 << 24)
+    v, sec = _median_rate(lambda: oracle.stable_sort_pairs_u64_u32(pk, pv, threads), pk.size)
+    out["pairs_par_stable_sort"] = {
+        "value": round(v, 4), "unit": "Gkeys/s", "cores": threads,
+        "sample": f"u64 keys + u32 values: per-thread std::stable_sort + stable merge-path "
+                  f"merges (rayon par_sort substitute), first 2^24 pairs of the metric input, "
+                  f"median of 5 ({sec:.3f} s)"}
+    pk, pv = pk[: 1 << 22], pv[: 1 << 22]
+    v, sec = _median_rate(lambda: oracle.stable_sort_pairs_u64_u32(pk, pv, 1), pk.size)
+    out["pairs_stable_sort_1core"] = {
+        "value": round(v, 4), "unit": "Gkeys/s", "cores": 1,
+        "sample": f"std::stable_sort of u64+u32 pairs by key (stable sort_by_key substitute), "
+                  f"first 2^22 metric pairs, median of 5 ({sec:.3f} s)"}
+    a, pa, b, pb = workloads.c4_merge_inputs(1 << 23)
+    v, sec = _median_rate(lambda: oracle.merge_pairs_u32(a, pa, b, pb), 2 * a.size)
+    out["merge_1core"] = {
+        "value": round(v, 4), "unit": "G outputs/s", "cores": 1,
+        "sample": f"std::merge of u32 keys + u32 payloads (the reference's two-pointer merge "
+                  f"substitute), C4 generator at 2^23 per side, median of 5 ({sec:.3f} s)"}
+    sa, sb = workloads.c5_inputs(1 << 22)
+    sets = {}
+    for op in ("union", "intersection", "difference", "symmetric_difference"):
+        v, sec = _median_rate(lambda op=op: oracle.std_set_op_u64(op, sa, sb), 2 * sa.size)
+        sets[op] = round(v, 4)
+    out["set_ops_1core"] = {
+        "value": sets, "unit": "G input keys/s", "cores": 1,
+        "sample": "std::set_union / set_intersection / set_difference / "
+                  "set_symmetric_difference (host_set_by substitute), C5 generator at 2^22 per "
+                  "side, median of 5 each"}
+    head.update(out)
+    return head
 
 
 # ---------------------------------------------------------------------------
@@ -240,7 +352,7 @@ def run_merge(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup):
     def step():
         cub.device_merge_pairs(launch, A, PA, B, PB, ws, out, outv)
 
-    ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, launch.stream(), steps, warmup, step)
+    ms, ms_min, wall, kms, launches, _ = _steps(torch, abi, launch.stream(), steps, warmup, step)
     total = 2 * n_each
     ok = _nondecreasing(torch, out.tensor, 32)
     ok = ok and _fingerprint(torch, out.tensor) == tuple(
@@ -276,7 +388,7 @@ def run_merge_sort(torch, np, cub, abi, DeviceBuffer, wd, log2n, steps, warmup):
     def step():
         cub.device_merge_sort_keys_copy(launch, src, ws, out)
 
-    ms, ms_min, wall, kms, launches, per_step = time_steps(torch, abi, launch.stream(), steps,
+    ms, ms_min, wall, kms, launches, per_step = _steps(torch, abi, launch.stream(), steps,
                                                            warmup, step)
     ok = _nondecreasing(torch, out.tensor, 32)
     ok = ok and _fingerprint(torch, out.tensor) == _fingerprint(torch, keys_t)
@@ -347,7 +459,7 @@ def run_set_ops(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup)
         def step(op=op, ws=ws):
             cub.device_set_keys(launch, op, A, B, ws, out)
 
-        ms, ms_min, wall, kms, _, _ = time_steps(torch, abi, launch.stream(), steps, warmup, step)
+        ms, ms_min, wall, kms, _, _ = _steps(torch, abi, launch.stream(), steps, warmup, step)
         m = ws.count()
         ok = m == want[op] and _nondecreasing(torch, out.tensor[:m], 64)
         results[op] = {
@@ -394,7 +506,7 @@ def run_record_sort(torch, np, abi, DeviceBuffer, wd, workloads, steps, warmup):
         abi.check(lib.rccl_hip_record_sort(arity, 8, rows.ptr, pay.ptr, rows.ptr, pay.ptr, n,
                                            ws.ptr, ws_bytes, launch.handle))
 
-    ms, ms_min, wall, kms, launches, per_step = time_steps(torch, abi, launch.stream(), steps,
+    ms, ms_min, wall, kms, launches, per_step = _steps(torch, abi, launch.stream(), steps,
                                                            warmup, step)
     host_rows = workloads.record_rows(arity, n)
     order = np.lexsort(host_rows.T[::-1])  # stable: equal rows keep index order
@@ -471,7 +583,7 @@ def run_compaction(torch, np, abi, DeviceBuffer, workloads, steps, warmup):
                                                      out_k.ptr, None, out_v.ptr, n, count.ptr,
                                                      ws.ptr, ws_bytes, handle))
 
-        ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, launch_stream, steps, warmup,
+        ms, ms_min, wall, kms, launches, _ = _steps(torch, abi, launch_stream, steps, warmup,
                                                         step)
         c = int(count.to_host_vec()[0])
         ok = c == groups and bool(np.array_equal(out_k.to_host_vec()[:c],
@@ -522,7 +634,7 @@ def run_search(torch, np, abi, DeviceBuffer, wd, log2_hay, log2_q, steps, warmup
         abi.check(lib.rccl_hip_bound_search(0, 1, 0, 0, hay.ptr, n, q.ptr, m, out.ptr, ws.ptr,
                                             ws_bytes, stream.cuda_stream))
 
-    ms, ms_min, wall, kms, launches, _ = time_steps(torch, abi, stream, steps, warmup, step)
+    ms, ms_min, wall, kms, launches, _ = _steps(torch, abi, stream, steps, warmup, step)
     # Validate against torch.searchsorted on the device (same definition).
     expect = torch.searchsorted(hay_t.to(torch.int64), q_t.to(torch.int64), right=False)
     ok = bool(torch.equal(out.tensor[:m], expect))
@@ -543,16 +655,32 @@ def run_search(torch, np, abi, DeviceBuffer, wd, log2_hay, log2_q, steps, warmup
     return res
 
 
+def run_c1_latency(torch, np, cub, abi, DeviceBuffer, wd, steps, warmup):
+    """C1 (2^20 u32 keys, cache-resident): latency of one in-place sort."""
+    n = 1 << 20
+    keys_t = wd.c1_keys(n)
+    r = run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, None, steps, warmup)
+    return {
+        "workload": "C1 DeviceRadixSort keys-only, 2^20 u32 uniform keys, ascending "
+                    "(cache-resident: latency, roofline informative only)",
+        "us_per_sort": round(r["ms"] * 1e3, 2), "us_per_sort_min": round(r["ms_min"] * 1e3, 2),
+        "value": round(n / (r["ms"] * 1e-3) / 1e9, 3), "unit": "Gkeys/s",
+        "launches": r["launches"], "kernel_ms": _rounded(r["kernel_ms"]),
+        "validated": r["validated"],
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=31)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--log2n", type=int, default=28)
     ap.add_argument("--no-pairs", action="store_true", help="skip the u64+u32 pairs leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the C1, C2 (uniform, low-entropy) and C3 legs")
     ap.add_argument("--no-ordering", action="store_true",
                     help="skip the C4 merge / merge sort and C5 set operation legs")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -595,7 +723,11 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(r32["ms"], 4),
+        "ms_per_step_mean": round(r32["ms_mean"], 4),
+        "ms_per_step_min": round(r32["ms_min"], 4),
         "ms_per_step_wall": round(r32["ms_wall"], 4),
+        "timing": "ms_per_step is the median of the timed steps' hipEvent intervals (the "
+                  "reference's protocol); the input is restored outside each interval",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -616,23 +748,50 @@ def main():
     }
     valid = r32["validated"]
     if rp is not None:
-        out["pairs"] = {
-            "value": round(n / (rp["ms"] * 1e-3) / 1e9, 3),
-            "unit": "Gkeys/s",
-            "ms_per_step": round(rp["ms"], 4),
-            "ms_per_step_wall": round(rp["ms_wall"], 4),
-            "dtype": "u64 keys + u32 values",
-            "config": {"workload": f"DeviceRadixSort pairs, u64 keys uniform over 64 bits, "
-                                   f"u32 values = index, n=2^{args.log2n}, 8 passes",
-                       "bytes_model": "200 B/pair = 8n + 8 x (12n read + 12n write)"},
-            "sort_roofline_frac": round(200.0 * n / (rp["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "roofline": roofline(24.0 * n, rp["kernel_ms"]["radix_onesweep"],
-                                 "radix_onesweep (one pass: 12n read + 12n write)",
-                                 profiled_traffic("radix_onesweep_pairs", args.log2n)),
-            "kernel_ms": _rounded(rp["kernel_ms"]),
-            "validated": rp["validated"],
-        }
+        out["pairs"] = radix_leg(
+            rp, n, f"DeviceRadixSort pairs, u64 keys uniform over 64 bits, u32 values = index, "
+                   f"n=2^{args.log2n}, 8 passes",
+            (200.0, "200 B/pair = 8n + 8 x (12n read + 12n write)"), 24.0,
+            "radix_onesweep (one pass: 12n read + 12n write)", "radix_onesweep_pairs",
+            args.log2n, "u64 keys + u32 values")
         valid = valid and rp["validated"]
+    if not args.no_configs:
+        log26 = max(args.log2n - 2, 1)
+        n26 = 1 << log26
+        configs = {}
+        _log("C1 latency")
+        configs["c1"] = run_c1_latency(torch, np, cub, abi, DeviceBuffer, wd, args.steps,
+                                       args.warmup)
+        for name, gen, label in (("c2_uniform", wd.c2_uniform, "uniform over 64 bits"),
+                                 ("c2_low_entropy", wd.c2_low_entropy,
+                                  "256 random values, Zipf s=1.1 frequencies")):
+            _log(name)
+            k, v = gen(n26)
+            r = run_radix(torch, np, cub, abi, DeviceBuffer, k, v, args.steps, args.warmup)
+            del k, v
+            configs[name] = radix_leg(
+                r, n26, f"C2 stable pair sort: 2^{log26} u64 keys ({label}), u32 values = "
+                        "original index, ascending; tie order checked exactly",
+                (200.0, "200 B/pair = 8n + 8 x (12n read + 12n write)"), 24.0,
+                "radix_onesweep (one pass: 12n read + 12n write)", "radix_onesweep_" + name,
+                args.log2n, "u64 keys + u32 values")
+            _log(f"{name}: {r['ms']:.3f} ms")
+        _log("c3")
+        k = wd.c3_keys(n).view(torch.int32)
+        r = run_radix(torch, np, cub, abi, DeviceBuffer, k, None, args.steps, args.warmup,
+                      kdt=np.float32, descending=True)
+        del k
+        configs["c3"] = radix_leg(
+            r, n, f"C3 f32 keys-only descending radix sort, 2^{args.log2n} keys ~ N(0, 1e3) "
+                  "with 1% +0.0, 1% -0.0, 0.1% +-inf, 0.1% denormals, 0.01% quiet NaN; bits "
+                  "checked exactly (order, multiset, signed-zero tie order)",
+            (36.0, "36 B/key = 4n (histogram read) + 4 x (4n read + 4n write)"), 8.0,
+            "radix_onesweep (one 8-bit pass: 4n read + 4n write)", "radix_onesweep_c3",
+            args.log2n, "f32 (ordered as u32 bits)")
+        _log(f"c3: {r['ms']:.3f} ms")
+        torch.cuda.empty_cache()
+        out["configs"] = configs
+        valid = valid and all(c["validated"] for c in configs.values())
     if not args.no_ordering:
         log_each = max(args.log2n - 1, 1)
         log_sort = max(args.log2n - 2, 1)
@@ -666,9 +825,7 @@ def main():
                                            "symmetric_difference"))
     if not args.no_cpu_baseline:
         _log("cpu baseline")
-        log_sample = min(26, args.log2n)
-        out["cpu_baseline"] = cpu_baseline(workloads.metric_u32_keys(1 << log_sample),
-                                           args.cpu_seconds, log_sample)
+        out["cpu_baseline"] = cpu_baseline()
     out["validated"] = bool(valid)
     print(json.dumps(out), flush=True)
     return 0 if valid else 1

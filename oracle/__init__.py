@@ -81,6 +81,15 @@ def _load():
         lib.oracle_sort_unstable_u32.argtypes = [c.c_void_p, c.c_size_t]
         lib.oracle_par_sort_unstable_u32.restype = c.c_int
         lib.oracle_par_sort_unstable_u32.argtypes = [c.c_void_p, c.c_size_t, c.c_int]
+        lib.oracle_stable_sort_pairs_u64_u32.restype = c.c_int
+        lib.oracle_stable_sort_pairs_u64_u32.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t,
+                                                         c.c_int]
+        lib.oracle_merge_pairs_u32.restype = c.c_int
+        lib.oracle_merge_pairs_u32.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p,
+                                               c.c_void_p, c.c_size_t, c.c_void_p, c.c_void_p]
+        lib.oracle_std_set_op_u64.restype = c.c_longlong
+        lib.oracle_std_set_op_u64.argtypes = [c.c_int, c.c_void_p, c.c_size_t, c.c_void_p,
+                                              c.c_size_t, c.c_void_p]
         _lib = lib
     return _lib
 
@@ -188,6 +197,42 @@ def par_sort_unstable_u32(keys, threads):
     if _load().oracle_par_sort_unstable_u32(_ptr(k), k.size, int(threads)) != 0:
         raise ValueError("oracle_par_sort_unstable_u32 failed")
     return k
+
+
+def stable_sort_pairs_u64_u32(keys, values, threads=1):
+    """Stable sort by key of copies of u64 `keys` and u32 `values` on
+    `threads` threads (the stable sort_by_key / par_sort substitute of the CPU
+    baseline; oracle_sort.cpp). Returns (keys, values)."""
+    k = np.ascontiguousarray(keys, dtype=np.uint64).copy()
+    v = np.ascontiguousarray(values, dtype=np.uint32).copy()
+    if k.size != v.size:
+        raise ValueError("keys and values differ in length")
+    if _load().oracle_stable_sort_pairs_u64_u32(_ptr(k), _ptr(v), k.size, int(threads)) != 0:
+        raise ValueError("oracle_stable_sort_pairs_u64_u32 failed")
+    return k, v
+
+
+def merge_pairs_u32(a, av, b, bv):
+    """std::merge of u32 keys with u32 payloads, first input first on ties
+    (the two-pointer merge substitute of the CPU baseline)."""
+    a, av, b, bv = (np.ascontiguousarray(x, dtype=np.uint32) for x in (a, av, b, bv))
+    out = np.empty(a.size + b.size, dtype=np.uint32)
+    outv = np.empty_like(out)
+    if _load().oracle_merge_pairs_u32(_ptr(a), _ptr(av), a.size, _ptr(b), _ptr(bv), b.size,
+                                      _ptr(out), _ptr(outv)) != 0:
+        raise ValueError("oracle_merge_pairs_u32 failed")
+    return out, outv
+
+
+def std_set_op_u64(op, a, b):
+    """std::set_* over sorted u64 multisets (the host_set_by substitute of
+    the CPU baseline). Returns the output keys."""
+    a, b = (np.ascontiguousarray(x, dtype=np.uint64) for x in (a, b))
+    out = np.empty(a.size + b.size, dtype=np.uint64)
+    n = _load().oracle_std_set_op_u64(SET_OPS[op], _ptr(a), a.size, _ptr(b), b.size, _ptr(out))
+    if n < 0:
+        raise ValueError("oracle_std_set_op_u64 failed")
+    return out[:n]
 
 
 def record_sort(rows, payloads=None):

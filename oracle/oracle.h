@@ -9,10 +9,19 @@
  * (paths are relative to the StarGazerM/rccl tree).
  *
  * Pinning (how each function is checked independently of its own formula):
- *   oracle_radix_*      reference literal vectors (signed/float/NaN/±0,
- *                       tests/golden), Python sorted() on integers and on
- *                       non-NaN floats (IEEE compare ties ±0 exactly like the
- *                       radix digit collapse), brute force on tiny inputs.
+ *   oracle_radix_*      reference literal vectors (tests/golden): signed keys,
+ *                       f32/f64 ±0/±inf keys and pairs, the f32/f64 NaN bit
+ *                       order ascending and descending, and the descending
+ *                       [-0.0, +0.0] -> [0x80000000, 0] known answer; the
+ *                       reference's unit rule that ±0 share every digit
+ *                       window in both orders (a stable two-zero sort is
+ *                       unchanged in every 1..8-bit window); Python's stable
+ *                       sorted() under a comparator written from IEEE 754
+ *                       totalOrder with ±0 tied (float compares for numbers,
+ *                       payload rules for NaNs of either sign); stable
+ *                       argsort and sorted() on integer keys and windows.
+ *                       A planted removal of the ±0 collapse fails all of
+ *                       the ±0 checks.
  *   oracle_merge        reference literal vectors, heapq.merge (stable,
  *                       first-iterable-first on ties).
  *   oracle_merge_sort   reference literal vectors, Python sorted() (stable).

@@ -82,6 +82,43 @@ rccl_hip_status check_launch(const char *role) {
   return RCCL_HIP_SUCCESS;
 }
 
+rccl_hip_status resident_blocks(const void *kernel, int threads, size_t *blocks) {
+  struct Entry {
+    int device;
+    const void *kernel;
+    int threads;
+    size_t blocks;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "current device", err);
+  std::lock_guard<std::mutex> lock(mu);
+  for (const Entry &e : cache) {
+    if (e.device == dev && e.kernel == kernel && e.threads == threads) {
+      *blocks = e.blocks;
+      return ok();
+    }
+  }
+  int cus = 0, per_cu = 0;
+  err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (err == hipSuccess)
+    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0);
+  if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "occupancy", err);
+  *blocks = size_t(cus) * size_t(per_cu > 0 ? per_cu : 0);
+  cache.push_back(Entry{dev, kernel, threads, *blocks});
+  return ok();
+}
+
+rccl_hip_status check_xcd_rows(const void *kernel, int threads, uint32_t run, const char *role) {
+  size_t blocks = 0;
+  RCCL_HIP_TRY(resident_blocks(kernel, threads, &blocks));
+  if (blocks < 2 * size_t(XCDS) * run)
+    return set_error(RCCL_HIP_ERROR_LAUNCH, role, 2 * XCDS * run, blocks);
+  return ok();
+}
+
 } // namespace rccl_hip
 
 extern "C" {

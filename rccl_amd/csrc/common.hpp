@@ -46,6 +46,16 @@ private:
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Blocks of `kernel` (launched with `threads` threads and no dynamic LDS) that
+// the current device holds at once: CUs x resident blocks per CU. Cached per
+// device and kernel.
+rccl_hip_status resident_blocks(const void *kernel, int threads, size_t *blocks);
+
+// The XCD-ordered look-back (xcd_order_tile) needs two rows of XCD runs
+// resident at once: RCCL_HIP_ERROR_LAUNCH where `kernel` cannot hold them, so
+// that a device too small for it reports an error instead of waiting forever.
+rccl_hip_status check_xcd_rows(const void *kernel, int threads, uint32_t run, const char *role);
+
 inline size_t key_bytes(rccl_hip_key_kind k) {
   switch (k) {
   case RCCL_HIP_KEY_U32: case RCCL_HIP_KEY_I32: case RCCL_HIP_KEY_F32: return 4;

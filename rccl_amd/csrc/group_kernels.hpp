@@ -328,6 +328,8 @@ rccl_hip_status run(const GroupArgs &a) {
   unsigned char *ws = static_cast<unsigned char *>(a.ws);
   uint64_t *desc = reinterpret_cast<uint64_t *>(ws + l.desc);
   const size_t words = lookback::state_words(l.tiles);
+  RCCL_HIP_TRY(check_xcd_rows(reinterpret_cast<const void *>(&group_tile_kernel<K, P, Op, ITEMS>),
+                              THREADS, XCD_RUN, "group tile does not fit on the device"));
   {
     KernelTimer t("group_clear", a.stream, words);
     group_clear_kernel<<<dim3(static_cast<uint32_t>(std::min<size_t>((words + 255) / 256, 1024))),

@@ -178,11 +178,16 @@ rccl_hip_status merge_sort_lowering(rccl_hip_key_kind key, size_t value_bytes, b
   a.end_bit = static_cast<uint32_t>(kb * 8);
   a.ws = ws + scratch;
   a.stream = stream;
-  if (in_keys != out_keys || (value_bytes && in_vals != out_vals)) {
-    a.src_keys = in_keys;
-    a.src_vals = value_bytes ? in_vals : nullptr;
-  }
+  // Keys and values may each be in place or not: the histogram and the first
+  // active pass read the input, and the plan keeps an in-place stream from
+  // being read and written by one pass.
+  a.src_keys = in_keys;
+  a.src_vals = value_bytes ? in_vals : nullptr;
   a.planned = true;
+  const bool vals_aliased = value_bytes && in_vals == out_vals;
+  const bool vals_copied = value_bytes && in_vals != out_vals;
+  a.plan_flags = (in_keys == out_keys || vals_aliased ? PLAN_IN_PLACE : 0u) |
+                 (in_keys != out_keys || vals_copied ? PLAN_COPIES : 0u);
   return sort_buffer(key, value_bytes,
                      descending ? RCCL_HIP_ORDER_DESCENDING : RCCL_HIP_ORDER_ASCENDING, a,
                      workspace_bytes - scratch - plan_bytes());

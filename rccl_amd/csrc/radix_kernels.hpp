@@ -289,20 +289,31 @@ struct PassPlan {
   uint32_t active, src, dst, lb;
 };
 
+// Plan flags: some stream (keys or values) is sorted in place (input ==
+// output), and some stream is not (its output must be written even when no
+// pass moves anything).
+constexpr uint32_t PLAN_IN_PLACE = 1u, PLAN_COPIES = 2u;
+
 // Thread-serial plan for P passes, `trivial` bit p set when pass p is
 // trivial. The active passes alternate between output and scratch so that
-// the last one writes the output; the first reads the input. In place (input
-// == output) the first must write the scratch, so the active count must be
-// even: a trivial pass is activated when it is odd (P is even, so one
-// exists). Otherwise at least one pass runs, a stable copy into the output.
-__device__ inline void assign_plan(int P, uint32_t trivial, uint32_t in_place,
+// the last one writes the output; the first reads the input. With a stream in
+// place the first must write the scratch, so the active count must be even:
+// a trivial pass is activated when it is odd (P is even, so one exists). When
+// no pass is active and another stream is not in place, two trivial passes
+// run (input -> scratch -> output: P >= 2), so that stream's output is
+// written too. Entirely out of place, at least one pass runs, a stable copy
+// into the output.
+__device__ inline void assign_plan(int P, uint32_t trivial, uint32_t flags,
                                    PassPlan *__restrict__ plan) {
   uint32_t act = ~trivial & ((P >= 32 ? 0u : (1u << P)) - 1u);
   int k = __builtin_popcount(act);
-  if (in_place) {
+  if (flags & PLAN_IN_PLACE) {
     if (k & 1) {
       act |= trivial & (0u - trivial);  // the lowest trivial pass
       ++k;
+    } else if (k == 0 && (flags & PLAN_COPIES)) {
+      act = 3u;  // every pass is trivial: the two lowest
+      k = 2;
     }
   } else if (k == 0) {
     act = 1u << (P - 1);
@@ -328,7 +339,8 @@ __device__ inline void assign_plan(int P, uint32_t trivial, uint32_t in_place,
 // plan. (Internal linkage, like init_kernel.)
 namespace {
 __global__ void __launch_bounds__(BINS)
-bins_scan_kernel(uint32_t *bins, uint32_t passes, uint32_t n, PassPlan *plan, uint32_t in_place) {
+bins_scan_kernel(uint32_t *bins, uint32_t passes, uint32_t n, PassPlan *plan,
+                 uint32_t plan_flags) {
   __shared__ uint32_t s_wave[BINS / 64];
   __shared__ uint32_t s_trivial;
   const uint32_t tid = threadIdx.x;
@@ -346,7 +358,7 @@ bins_scan_kernel(uint32_t *bins, uint32_t passes, uint32_t n, PassPlan *plan, ui
     bins[p * BINS + tid] = excl;
     __syncthreads();
   }
-  if (plan && tid == 0) assign_plan(static_cast<int>(passes), s_trivial, in_place, plan);
+  if (plan && tid == 0) assign_plan(static_cast<int>(passes), s_trivial, plan_flags, plan);
 }
 } // namespace
 
@@ -810,10 +822,13 @@ struct SortArgs {
   const void *src_keys = nullptr;
   const void *src_vals = nullptr;
   // Planned sorts skip trivial passes: keys[0] / vals[0] are the output,
-  // keys[1] / vals[1] the scratch, src_keys / src_vals the input (null: in
-  // place). The result always ends in the output. The plan needs
-  // plan_bytes() of workspace after the layout's.
+  // keys[1] / vals[1] the scratch, src_keys / src_vals the input (either may
+  // equal its output: in place). plan_flags says whether some stream is in
+  // place and whether some is not (PLAN_IN_PLACE, PLAN_COPIES). The result
+  // always ends in the output. The plan needs plan_bytes() of workspace after
+  // the layout's.
   bool planned = false;
+  uint32_t plan_flags = 0;
 };
 
 inline size_t plan_bytes() { return align_up(8 * sizeof(PassPlan), 256); }
@@ -865,7 +880,7 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
   {
     KernelTimer t("radix_bins_scan", a.stream, passes * BINS);
     bins_scan_kernel<<<1, BINS, 0, a.stream>>>(bins, passes, static_cast<uint32_t>(a.n), plan,
-                                                a.src_keys ? 0u : 1u);
+                                                a.plan_flags);
   }
   RCCL_HIP_TRY(check_launch("radix bins scan"));
 

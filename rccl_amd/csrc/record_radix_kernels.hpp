@@ -85,7 +85,7 @@ static_assert(HIST_THREADS >= BINS, "the plan uses one thread per digit");
 // every thread of one block; threads past BINS only join the barriers.
 template <int N>
 __device__ __forceinline__ void write_plan(uint32_t *__restrict__ bins, uint32_t n,
-                                           PassPlan *__restrict__ plan, uint32_t in_place) {
+                                           PassPlan *__restrict__ plan, uint32_t plan_flags) {
   constexpr int P = 4 * N;
   __shared__ uint32_t s_wave[P][BINS / 64];
   __shared__ uint32_t s_trivial[P];
@@ -118,7 +118,7 @@ __device__ __forceinline__ void write_plan(uint32_t *__restrict__ bins, uint32_t
   if (tid != 0) return;
   uint32_t trivial = 0;
   for (int p = 0; p < P; ++p) trivial |= s_trivial[p] ? (1u << p) : 0u;
-  radix::assign_plan(P, trivial, in_place, plan);
+  radix::assign_plan(P, trivial, plan_flags, plan);
 }
 
 // Adds one wave's digits of byte `byte` of a column word to the LDS
@@ -141,7 +141,7 @@ __device__ __forceinline__ void count_byte(uint32_t *h, uint32_t w, uint32_t w0,
 template <int N>
 __global__ void __launch_bounds__(HIST_THREADS)
 row_histogram_kernel(const Row<N> *__restrict__ rows, size_t n, uint32_t *__restrict__ bins,
-                     uint32_t *__restrict__ done, PassPlan *__restrict__ plan, uint32_t in_place,
+                     uint32_t *__restrict__ done, PassPlan *__restrict__ plan, uint32_t plan_flags,
                      uint32_t *__restrict__ zero_words, size_t zero_count) {
   constexpr int P = 4 * N;
   __shared__ uint32_t hist[P * BINS];  // [pass][digit], pass 0 = last column's low byte
@@ -194,7 +194,7 @@ row_histogram_kernel(const Row<N> *__restrict__ rows, size_t n, uint32_t *__rest
                  : 0u;
   __syncthreads();
   if (!s_last) return;
-  write_plan<N>(bins, static_cast<uint32_t>(n), plan, in_place);
+  write_plan<N>(bins, static_cast<uint32_t>(n), plan, plan_flags);
 }
 
 // ---------------------------------------------------------------------------
@@ -326,10 +326,14 @@ rccl_hip_status run_radix(const RecordArgs &a) {
     const size_t blocks =
         std::max<size_t>(1, std::min<size_t>((a.n + chunk - 1) / chunk, size_t(cus)));
     // Rows or payloads sorted in place: the first active pass must not write
-    // the buffer it reads.
-    const bool in_place = a.in == a.out || (a.in_v != nullptr && a.in_v == a.out_v);
+    // the buffer it reads. Rows or payloads out of place: their output must
+    // be written even when every row is equal.
+    const bool has_v = a.in_v != nullptr;
+    const uint32_t flags =
+        (a.in == a.out || (has_v && a.in_v == a.out_v) ? radix::PLAN_IN_PLACE : 0u) |
+        (a.in != a.out || (has_v && a.in_v != a.out_v) ? radix::PLAN_COPIES : 0u);
     row_histogram_kernel<N><<<dim3(static_cast<uint32_t>(blocks)), HIST_THREADS, 0, a.stream>>>(
-        b.in, a.n, bins, bins + P * BINS, plan, in_place ? 1u : 0u, lb[0].tile,
+        b.in, a.n, bins, bins + P * BINS, plan, flags, lb[0].tile,
         l.lb_bytes / sizeof(uint32_t));
   }
   RCCL_HIP_TRY(check_launch("record sort histogram"));

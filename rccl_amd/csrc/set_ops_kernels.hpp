@@ -425,6 +425,10 @@ rccl_hip_status run_op(const SetArgs &s) {
   uint64_t *ginc = reinterpret_cast<uint64_t *>(ws + l.ginc);
   // Descriptors and group words are contiguous.
   const size_t state_words = l.tiles + 2 * l.groups;
+  RCCL_HIP_TRY(check_xcd_rows(
+      s.arith ? reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, true>)
+              : reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, false>),
+      THREADS, XCD_RUN, "set tile does not fit on the device"));
   {
     KernelTimer t("set_clear", s.stream, state_words);
     clear_kernel<<<dim3(static_cast<uint32_t>(std::min<size_t>((state_words + 255) / 256, 1024))),

@@ -40,13 +40,77 @@ def descending(a, b):
     return (b > a) - (b < a)
 
 
-def order_code(order) -> int:
-    """Lower a comparator to its prebuilt kernel variant."""
-    if order is None or order is ascending or order == ASCENDING:
+class ComparatorNotLowered(ValueError):
+    """A comparator closure that is neither the natural order nor its reverse
+    on the probe keys. Only those two orders have prebuilt kernels, and there
+    is no host fallback, so the call is rejected before any launch."""
+
+
+def _probe_keys(dtype):
+    """Fixed probe keys for classifying a comparator over `dtype`: the type's
+    extremes and their neighbours, zero and small values (runs of equal
+    decades and both parities), byte boundaries; for floats also the
+    infinities, signed zeros, denormals and the smallest normals."""
+    dt = np.dtype(dtype)
+    if dt.kind == "f":
+        fi = np.finfo(dt)
+        tiny, sub = float(fi.tiny), float(fi.smallest_subnormal)
+        vals = [-np.inf, -float(fi.max), -1.5, -1.0, -tiny, -sub, -0.0, 0.0, sub, tiny, 0.5,
+                1.0, 1.5, 2.0, 10.0, 14.0, 15.0, 16.0, 25.0, 26.0, float(fi.max), np.inf]
+    else:
+        ii = np.iinfo(dt)
+        small = list(range(0, 22)) + [126, 127, 128, 129, 255, 256]
+        vals = [ii.min, ii.min + 1, ii.max - 1, ii.max, ii.max // 2, ii.max // 2 + 1]
+        vals += [v for v in small if v <= ii.max]
+        if ii.min < 0:
+            vals += [-v for v in small if -v >= ii.min]
+    # Distinct bit patterns (-0.0 and +0.0 both stay), as Python scalars
+    # (float keys widen exactly), which is what a Python closure expects.
+    arr = np.array(vals, dtype=dt)
+    _, first = np.unique(arr.view(f"u{dt.itemsize}"), return_index=True)
+    conv = float if dt.kind == "f" else int
+    return [conv(arr[i]) for i in sorted(first)]
+
+
+def _sign(x) -> int:
+    return (x > 0) - (x < 0)
+
+
+def order_code(order, dtype=None) -> int:
+    """Lower a comparator to its prebuilt kernel variant.
+
+    ``ascending`` / ``descending`` (or the ABI codes) map directly. Any other
+    closure ``f(a, b) -> negative | 0 | positive`` (Rust's Ordering as a
+    sign) is classified by evaluating it on every pair of the probe keys of
+    ``dtype``: if it agrees with the natural order everywhere it lowers to
+    ASCENDING, if with the reversed order DESCENDING; otherwise
+    ComparatorNotLowered is raised. For floats the natural order is IEEE
+    comparison, so -0.0 and +0.0 are equivalent: a closure that orders them
+    (Rust's total_cmp) is rejected rather than silently changed."""
+    if order is None or order is ascending:
         return ASCENDING
-    if order is descending or order == DESCENDING:
+    if order is descending:
         return DESCENDING
-    raise ValueError("only the ascending and descending orders have prebuilt kernels")
+    if isinstance(order, (int, np.integer)) and not isinstance(order, bool):
+        if int(order) in (ASCENDING, DESCENDING):
+            return int(order)
+        raise ValueError(f"unknown order code {order}")
+    if not callable(order):
+        raise TypeError("an order is a comparator closure or an order code")
+    probes = _probe_keys(np.uint32 if dtype is None else dtype)
+    asc = desc = True
+    for a in probes:
+        for b in probes:
+            got = _sign(order(a, b))
+            nat = _sign(ascending(a, b))
+            asc = asc and got == nat
+            desc = desc and got == -nat
+            if not (asc or desc):
+                raise ComparatorNotLowered(
+                    "the comparator is neither the natural order nor its reverse on the probe "
+                    f"keys (it returned {got} for ({a!r}, {b!r})); only those orders have "
+                    "prebuilt kernels")
+    return ASCENDING if asc else DESCENDING
 
 
 class Program:
@@ -294,8 +358,8 @@ def device_merge_keys(launch, first, second, workspace, output, order=ascending)
     kind = _ordering_kind(first.dtype)
     wptr, wbytes = _ws_ptr(workspace)
     _abi.check(_abi.load().rccl_hip_merge(
-        _abi.KEY_KINDS[kind], 0, order_code(order), first.ptr, None, first.len(), second.ptr,
-        None, second.len(), output.ptr, None, wptr, wbytes, launch.handle))
+        _abi.KEY_KINDS[kind], 0, order_code(order, first.dtype), first.ptr, None, first.len(),
+        second.ptr, None, second.len(), output.ptr, None, wptr, wbytes, launch.handle))
 
 
 def device_merge_pairs(launch, first_keys, first_values, second_keys, second_values, workspace,
@@ -308,7 +372,8 @@ def device_merge_pairs(launch, first_keys, first_values, second_keys, second_val
     kind = _ordering_kind(first_keys.dtype)
     wptr, wbytes = _ws_ptr(workspace)
     _abi.check(_abi.load().rccl_hip_merge(
-        _abi.KEY_KINDS[kind], first_values.dtype.itemsize, order_code(order), first_keys.ptr,
+        _abi.KEY_KINDS[kind], first_values.dtype.itemsize, order_code(order, first_keys.dtype),
+        first_keys.ptr,
         first_values.ptr, first_keys.len(), second_keys.ptr, second_values.ptr,
         second_keys.len(), output_keys.ptr, output_values.ptr, wptr, wbytes, launch.handle))
 
@@ -344,7 +409,7 @@ def _merge_sort(launch, in_keys, in_values, out_keys, out_values, ws, order):
     vb = 0 if in_values is None else in_values.dtype.itemsize
     wptr, wbytes = _ws_ptr(ws)
     _abi.check(_abi.load().rccl_hip_merge_sort(
-        _abi.KEY_KINDS[kind], vb, order_code(order), in_keys.ptr,
+        _abi.KEY_KINDS[kind], vb, order_code(order, in_keys.dtype), in_keys.ptr,
         None if in_values is None else in_values.ptr, out_keys.ptr,
         None if out_values is None else out_values.ptr, n, wptr, wbytes, launch.handle))
 
@@ -423,7 +488,7 @@ def _set_op(launch, op, first_keys, first_values, second_keys, second_values, ws
         _check_len("set output values", output_keys.len(), output_values.len())
         vb = first_values.dtype.itemsize
     _abi.check(_abi.load().rccl_hip_set_op(
-        op, _abi.KEY_KINDS[kind], vb, order_code(order), first_keys.ptr,
+        op, _abi.KEY_KINDS[kind], vb, order_code(order, first_keys.dtype), first_keys.ptr,
         None if first_values is None else first_values.ptr, first_keys.len(), second_keys.ptr,
         None if second_values is None else second_values.ptr, second_keys.len(),
         None if output_keys is None else output_keys.ptr,
@@ -480,7 +545,7 @@ def device_set_arithmetic(launch, operation, first: ArithmeticRange, second: Ari
     b0 = np.ascontiguousarray(np.array([second.start, second.step], dtype=second.dtype))
     w = first.dtype.itemsize
     _abi.check(_abi.load().rccl_hip_set_op_arithmetic(
-        SET_OPERATIONS[operation], _abi.KEY_KINDS[kind], order_code(order),
+        SET_OPERATIONS[operation], _abi.KEY_KINDS[kind], order_code(order, first.dtype),
         a0.ctypes.data, a0.ctypes.data + w, first.len(), b0.ctypes.data, b0.ctypes.data + w,
         second.len(), None if output is None else output.ptr,
         0 if output is None else output.len(), workspace.output_count.ptr, workspace.control.ptr,

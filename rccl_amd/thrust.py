@@ -64,6 +64,23 @@ class Execution:
 # ---------------------------------------------------------------------------
 # Views.
 # ---------------------------------------------------------------------------
+class _SortMethodsForward:
+    """Sort methods of a mutable view (the reference calls them on the
+    DeviceBuffer itself: rccl-thrust/src/ordering.rs:46-89)."""
+
+    def sort_unstable(self, execution: "Execution") -> None:
+        sort_unstable(self, execution)
+
+    def sort(self, execution: "Execution") -> None:
+        sort(self, execution)
+
+    def sort_unstable_by(self, execution: "Execution", order) -> None:
+        sort_unstable_by(self, execution, order)
+
+    def sort_by(self, execution: "Execution", order) -> None:
+        sort_by(self, execution, order)
+
+
 class DeviceView:
     def __init__(self, buffer: DeviceBuffer):
         self.buffer = buffer
@@ -108,7 +125,7 @@ class DeviceView:
         return _SetExpression("symmetric_difference", self, second, order)
 
 
-class DeviceViewMut(DeviceView):
+class DeviceViewMut(DeviceView, _SortMethodsForward):
     def as_view(self) -> DeviceView:
         return DeviceView(self.buffer)
 
@@ -160,7 +177,25 @@ class KeyValueRange:
         return _SetExpression("symmetric_difference", self, second, order)
 
 
-class KeyValueRangeMut(KeyValueRange):
+class _SortMethods:
+    """DeviceSortExt / DeviceKeyValueSortExt (rccl-thrust/src/ordering.rs:13-182):
+    natural-order sorts take the radix sort, comparator sorts the stable
+    merge sort; every call synchronizes."""
+
+    def sort_unstable(self, execution: "Execution") -> None:
+        sort_unstable(self, execution)
+
+    def sort(self, execution: "Execution") -> None:
+        sort(self, execution)
+
+    def sort_unstable_by(self, execution: "Execution", order) -> None:
+        sort_unstable_by(self, execution, order)
+
+    def sort_by(self, execution: "Execution", order) -> None:
+        sort_by(self, execution, order)
+
+
+class KeyValueRangeMut(KeyValueRange, _SortMethods):
     pass
 
 
@@ -232,6 +267,7 @@ def _radix(execution: Execution, target) -> None:
 
 def _merge_sort(execution: Execution, target, order) -> None:
     keys, values = _split(target)
+    cub.order_code(order, keys.dtype)  # rejects an unsupported closure before any allocation
     launch = execution.launch()
     if values is None:
         ws = cub.device_merge_sort_workspace(launch, keys.dtype, keys.len())
@@ -491,7 +527,8 @@ def _bound(execution, haystack, needles, output, order, upper):
     nbytes = _abi.workspace_bytes("rccl_hip_bound_search_workspace_bytes", kind, arity, h.len())
     ws = DeviceBuffer.bytes(nbytes, execution.launch().program.device)
     _abi.check(_abi.load().rccl_hip_bound_search(
-        kind, arity, cub.order_code(order), int(upper), h.ptr, h.len(), q.ptr, q.len(), out.ptr,
+        kind, arity, cub.order_code(order, np.uint32 if arity > 1 else h.dtype), int(upper), h.ptr,
+        h.len(), q.ptr, q.len(), out.ptr,
         ws.ptr, nbytes, execution.launch().handle))
     execution.synchronize()
 

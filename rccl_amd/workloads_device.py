@@ -52,6 +52,10 @@ def sort_u64(x: torch.Tensor) -> torch.Tensor:
     return torch.sort(x ^ _SIGN).values ^ _SIGN
 
 
+def c1_keys(n: int = 1 << 20, device="cuda") -> torch.Tensor:
+    return shr(hash_range(SEEDS["C1"], n, device=device), 32).to(torch.int32)
+
+
 def metric_u32_keys(n: int = 1 << 28, device="cuda") -> torch.Tensor:
     return shr(hash_range(SEEDS["M32"], n, device=device), 32).to(torch.int32)
 
@@ -59,6 +63,74 @@ def metric_u32_keys(n: int = 1 << 28, device="cuda") -> torch.Tensor:
 def metric_pairs(n: int = 1 << 28, device="cuda"):
     keys = hash_range(SEEDS["M64"], n, device=device)
     return keys, torch.arange(n, dtype=torch.int32, device=device)
+
+
+def c2_uniform(n: int = 1 << 26, device="cuda"):
+    keys = hash_range(SEEDS["C2"], n, device=device)
+    return keys, torch.arange(n, dtype=torch.int32, device=device)
+
+
+def c2_low_entropy(n: int = 1 << 26, device="cuda"):
+    """Device twin of workloads.c2_low_entropy (bit-identical: the uniforms are
+    exact 53-bit values and the inverse CDF is a comparison search over the
+    same float64 table)."""
+    import numpy as np
+
+    dictionary = hash_range(SEEDS["C2_dict"], 256, device=device)
+    weights = np.arange(1, 257, dtype=np.float64) ** -1.1
+    cdf_h = np.cumsum(weights / weights.sum())
+    cdf_h[-1] = 1.0
+    cdf = torch.from_numpy(cdf_h).to(device)
+    u = shr(hash_range(SEEDS["C2_zipf"], n, device=device), 11).to(torch.float64) * 2.0 ** -53
+    idx = torch.searchsorted(cdf, u, right=True).clamp_(max=255)
+    del u
+    return dictionary[idx], torch.arange(n, dtype=torch.int32, device=device)
+
+
+def c3_keys(n: int = 1 << 28, device="cuda") -> torch.Tensor:
+    """Device twin of workloads.c3_keys, as float32. The special values and
+    their positions are bit-identical to the host generator's; the Box-Muller
+    normals are computed with the device's float64 log/sqrt/cos, which may
+    differ from the host libm in the last float64 place, and so (rarely) in
+    the last float32 place of a normal value."""
+    import math
+
+    seed = SEEDS["C3"]
+    out = torch.empty(n, dtype=torch.float32, device=device)
+    chunk = 1 << 24
+    for lo in range(0, n, chunk):
+        hi = min(n, lo + chunk)
+        idx = torch.arange(lo, hi, dtype=torch.int64, device=device)
+        a = splitmix64(idx * 2 + _signed(seed))
+        b = splitmix64(idx * 2 + _signed(seed + 1))
+        u1 = (shr(a, 11).to(torch.float64) + 1.0) * 2.0 ** -53
+        u2 = shr(b, 11).to(torch.float64) * 2.0 ** -53
+        z = torch.sqrt(-2.0 * torch.log(u1)) * torch.cos(2.0 * math.pi * u2)
+        out[lo:hi] = (1000.0 * z).to(torch.float32)
+    bits = out.view(torch.int32)
+    from .workloads import c3_special_counts
+
+    counts = c3_special_counts(n)
+    total = sum(counts.values())
+    prio = hash_range(SEEDS["C3_pos"], n, device=device)
+    # The `total` positions of smallest unsigned priority, in priority order.
+    chosen = torch.sort(prio ^ _SIGN).indices[:total]
+    del prio
+    pos = 0
+    sel = {}
+    for name in ("+0", "-0", "+inf", "-inf", "denormal", "nan"):
+        sel[name] = chosen[pos:pos + counts[name]]
+        pos += counts[name]
+    bits[sel["+0"]] = 0
+    bits[sel["-0"]] = _signed32(0x80000000)
+    bits[sel["+inf"]] = 0x7F800000
+    bits[sel["-inf"]] = _signed32(0xFF800000)
+    d = hash_range(SEEDS["C3_pos"] ^ 0xDE40, counts["denormal"], device=device)
+    mant = _u64_mod(d, (1 << 23) - 1) + 1
+    sign = shr(d, 63) << 31
+    bits[sel["denormal"]] = _u32_bits(sign | mant)
+    bits[sel["nan"]] = 0x7FC00000
+    return out
 
 
 def _sorted_u32_24bit(n: int, seed: int, device) -> torch.Tensor:
@@ -74,6 +146,11 @@ def c4_merge_inputs(n_each: int = 1 << 27, device="cuda"):
     pa = torch.arange(n_each, dtype=torch.int32, device=device)
     pb = pa | _signed32(0x80000000)
     return a, pa, b, pb
+
+
+def _u32_bits(v: torch.Tensor) -> torch.Tensor:
+    """int32 bit patterns of int64 values in [0, 2^32)."""
+    return (v - (v >= (1 << 31)).to(torch.int64) * (1 << 32)).to(torch.int32)
 
 
 def _signed32(u: int) -> int:

@@ -371,3 +371,47 @@ def test_bound_search_workspace_and_validation(lib):
                                      None) == 2
     assert lib.rccl_hip_bound_search(0, 1, 0, 0, FAKE, n, FAKE, m, FAKE, None, 0, None) == 2
     assert lib.rccl_hip_bound_search(0, 1, 0, 0, FAKE, n, FAKE, 0, FAKE, None, 0, None) == 0
+
+
+def test_comparator_classification():
+    """Closures lower to the prebuilt ascending / descending kernels by
+    probing, whatever their identity; the reference's custom comparators
+    (rccl-thrust/examples/sort.rs:36-49,100-112) and a float total order that
+    separates the signed zeros are rejected."""
+    import struct
+
+    from rccl_amd import cub
+
+    def rust_cmp(a, b):
+        return (a > b) - (a < b)
+
+    for dt in (np.uint8, np.int16, np.uint32, np.int64, np.float32, np.float64):
+        assert cub.order_code(lambda a, b: rust_cmp(a, b), dt) == cub.ASCENDING
+        assert cub.order_code(lambda a, b: rust_cmp(b, a), dt) == cub.DESCENDING
+        assert cub.order_code(lambda a, b: -1 if a < b else (1 if a > b else 0), dt) == 0
+    assert cub.order_code(cub.descending) == cub.DESCENDING
+    assert cub.order_code(None) == cub.ASCENDING
+    assert cub.order_code(cub.DESCENDING) == cub.DESCENDING
+    custom = [
+        lambda l, r: -1 if (l & 1) == 0 and (r & 1) != 0 else
+        (1 if (l & 1) != 0 and (r & 1) == 0 else rust_cmp(l, r)),
+        lambda l, r: rust_cmp(l & 1, r & 1) or rust_cmp(l, r),
+        lambda l, r: rust_cmp(l // 10, r // 10),
+        lambda l, r: 0,
+        lambda l, r: rust_cmp(abs(l), abs(r)),
+    ]
+    for f in custom:
+        with pytest.raises(cub.ComparatorNotLowered):
+            cub.order_code(f, np.int32)
+
+    def total_cmp(a, b):
+        ka, kb = (struct.unpack("<i", struct.pack("<f", x))[0] for x in (a, b))
+        ka ^= (ka >> 31) & 0x7FFFFFFF
+        kb ^= (kb >> 31) & 0x7FFFFFFF
+        return rust_cmp(ka, kb)
+
+    with pytest.raises(cub.ComparatorNotLowered):
+        cub.order_code(total_cmp, np.float32)
+    with pytest.raises(ValueError):
+        cub.order_code(7)
+

@@ -314,3 +314,38 @@ def test_merge_sort_radix_lowering_trivial_passes(launch, kind, shape):
             assert np.array_equal(gv, wv), (shape, descending, copy)
         got = _merge_sort(launch, keys, descending=descending, copy=True)
         assert np.array_equal(_bits(got), _bits(wk)), (shape, descending)
+
+
+@pytest.mark.parametrize("kind", ["u32", "u64"])
+@pytest.mark.parametrize("alias", ["keys", "values"])
+@pytest.mark.parametrize("shape", ["one_byte", "constant", "full"])
+def test_merge_sort_radix_lowering_mixed_aliasing(launch, kind, alias, shape):
+    """Above the lowering threshold, keys in place with values copied (or the
+    reverse): the plan must not let one pass read and write the in-place
+    stream, and must write the copied stream even when no pass is needed."""
+    from rccl_amd import _abi
+
+    n = 131_075
+    dt = np.dtype(DTYPES[kind])
+    raw = workloads.hash_range(4242, n)
+    if shape == "one_byte":
+        keys = (raw >> np.uint64(56)).astype(dt)  # an odd active-pass count (one)
+    elif shape == "constant":
+        keys = np.full(n, 9, dtype=dt)
+    else:
+        keys = (raw >> np.uint64(64 - 8 * dt.itemsize)).astype(dt)
+    vals = np.arange(n, dtype=np.uint32)
+    wk, wv = oracle.merge_sort(kind, keys, vals, False)
+    k_in, v_in = _dev(keys), _dev(vals)
+    if alias == "keys":
+        k_out, v_out = k_in, DeviceBuffer.zeroed(np.uint32, n)
+    else:
+        k_out, v_out = DeviceBuffer.zeroed(dt, n), v_in
+    ws = cub.device_merge_sort_pairs_workspace(launch, dt, np.uint32, n)
+    wptr, wbytes = cub._ws_ptr(ws)
+    _abi.check(_abi.load().rccl_hip_merge_sort(_abi.KEY_KINDS[kind], 4, 0, k_in.ptr, v_in.ptr,
+                                               k_out.ptr, v_out.ptr, n, wptr, wbytes,
+                                               launch.handle))
+    launch.synchronize()
+    np.testing.assert_array_equal(k_out.to_host_vec(), wk)
+    np.testing.assert_array_equal(v_out.to_host_vec(), wv)

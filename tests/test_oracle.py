@@ -217,6 +217,87 @@ def test_radix_oracle_vs_numpy(kind, descending):
         assert np.array_equal(got_v, want_v), (begin, end)
 
 
+@pytest.mark.parametrize("kind", ["f32", "f64"])
+@pytest.mark.parametrize("descending", [False, True])
+def test_radix_oracle_signed_zero_tie_every_window(kind, descending):
+    """rccl-cub/src/ordering_backend/tests.rs:135-172 requires +0.0 and -0.0
+    to have equal digits in every window (1 to 8 bits at every position) and
+    in both orders. As a sort: a two-key input of opposite-signed zeros is a
+    tie in every bit window, so a stable sort leaves it unchanged, whichever
+    zero comes first. Without the collapse, some window separates them."""
+    dt = np.dtype(NP[kind])
+    width = 8 * dt.itemsize
+    for first, second in ((0.0, -0.0), (-0.0, 0.0)):
+        keys = np.array([first, second], dtype=dt)
+        for begin in range(width):
+            for end in range(begin + 1, min(width, begin + 8) + 1):
+                got = oracle.radix_sort(kind, keys, None, descending, begin, end)
+                assert np.array_equal(_bits(got), _bits(keys)), (first, begin, end)
+
+
+def _ieee_total_order_tied_zeros(bits_a, bits_b, width):
+    """IEEE 754-2008 totalOrder (section 5.10) with -0 and +0 tied: numbers by
+    value (IEEE <); negative NaNs below every number and positive NaNs above;
+    among NaNs of one sign, the larger payload lies further from zero."""
+    import struct
+
+    fmt = {32: ("<I", "<f"), 64: ("<Q", "<d")}[width]
+    a = struct.unpack(fmt[1], struct.pack(fmt[0], bits_a))[0]
+    b = struct.unpack(fmt[1], struct.pack(fmt[0], bits_b))[0]
+    sign = 1 << (width - 1)
+
+    def cls(bits, x):
+        if x != x:
+            return 0 if bits & sign else 2
+        return 1
+
+    ca, cb = cls(bits_a, a), cls(bits_b, b)
+    if ca != cb:
+        return -1 if ca < cb else 1
+    if ca == 1:
+        return -1 if a < b else (1 if a > b else 0)
+    pa, pb = bits_a & (sign - 1), bits_b & (sign - 1)
+    if ca == 0:  # negative NaNs: larger payload first
+        pa, pb = pb, pa
+    return -1 if pa < pb else (1 if pa > pb else 0)
+
+
+@pytest.mark.parametrize("kind", ["f32", "f64"])
+@pytest.mark.parametrize("descending", [False, True])
+def test_radix_oracle_float_order_vs_python_sorted(kind, descending):
+    """The float radix order is IEEE totalOrder with -0.0 and +0.0 tied, as a
+    stable sort: checked against Python's stable sorted() under a comparator
+    written from that definition (float comparisons for numbers, payload
+    rules for NaN), on keys with many interleaved signed zeros, infinities,
+    denormals, extremes and NaNs of both signs and several payloads."""
+    import functools
+
+    n = 6000
+    dt = np.dtype(NP[kind])
+    ut = BITS_OF[dt.itemsize]
+    width = 8 * dt.itemsize
+    keys = _special_float_keys(kind, n, 901 + width).copy()
+    bits = keys.view(ut)
+    rng = np.random.default_rng(77 + width)
+    sign = ut(1) << ut(width - 1)
+    exp_all = ut((1 << (width - 1)) - 1) ^ ut((1 << (23 if width == 32 else 52)) - 1)
+    zpos = rng.integers(0, n, size=n // 5)
+    bits[zpos] = np.where(rng.integers(0, 2, size=zpos.size) == 1, sign, ut(0)).astype(ut)
+    npos = rng.integers(0, n, size=n // 50)
+    payload = rng.integers(1, 4, size=npos.size).astype(ut)
+    quiet = ut(1) << ut((22 if width == 32 else 51))
+    nan_bits = exp_all | payload | np.where(rng.integers(0, 2, size=npos.size) == 1, quiet,
+                                            ut(0)).astype(ut)
+    bits[npos] = np.where(rng.integers(0, 2, size=npos.size) == 1, nan_bits | sign, nan_bits)
+    idx = np.arange(n, dtype=np.uint32)
+    cmp = functools.cmp_to_key(
+        lambda i, j: _ieee_total_order_tied_zeros(int(bits[i]), int(bits[j]), width))
+    want = sorted(range(n), key=cmp, reverse=descending)  # stable in both directions
+    got_k, got_v = oracle.radix_sort(kind, keys, idx, descending)
+    assert got_v.tolist() == want
+    assert np.array_equal(_bits(got_k), bits[np.array(want)])
+
+
 def test_radix_oracle_pairs_probe_family():
     # rccl-cub/examples/device_radix_sort_pairs_probe.rs:34-176: narrow key
     # domain, Rust's stable sort_by_key as the reference.
@@ -381,6 +462,38 @@ def test_cpu_baseline_sorts_vs_numpy(n, threads):
     want = np.sort(keys)
     assert np.array_equal(oracle.sort_unstable_u32(keys), want)
     assert np.array_equal(oracle.par_sort_unstable_u32(keys, threads), want)
+
+
+@pytest.mark.parametrize("n", [0, 1, 7, 1000, 65537, 1 << 19])
+@pytest.mark.parametrize("threads", [1, 3, 16])
+def test_cpu_baseline_stable_pairs_vs_numpy(n, threads):
+    """The stable pair sort substitute (one thread: std::stable_sort; more:
+    chunk stable sorts + stable merge-path merges) against numpy's stable
+    argsort, with heavy ties crossing chunk boundaries."""
+    rng = np.random.default_rng(n * 7 + threads)
+    keys = rng.integers(0, max(1, n // 16) + 1, size=n, dtype=np.uint64)
+    keys[::5] = rng.integers(0, 1 << 63, size=keys[::5].size, dtype=np.uint64) << np.uint64(1)
+    vals = np.arange(n, dtype=np.uint32)
+    order = np.argsort(keys, kind="stable")
+    gk, gv = oracle.stable_sort_pairs_u64_u32(keys, vals, threads)
+    assert np.array_equal(gk, keys[order]) and np.array_equal(gv, vals[order])
+
+
+def test_cpu_baseline_merge_and_set_ops_vs_oracle():
+    """The std::merge / std::set_* substitutes agree with the oracle's
+    restatements of the reference's merge and host_set_by."""
+    rng = np.random.default_rng(5)
+    a = np.sort(rng.integers(0, 500, size=4000).astype(np.uint32))
+    b = np.sort(rng.integers(0, 500, size=3000).astype(np.uint32))
+    av = np.arange(a.size, dtype=np.uint32)
+    bv = np.arange(b.size, dtype=np.uint32) | np.uint32(1 << 31)
+    gk, gv = oracle.merge_pairs_u32(a, av, b, bv)
+    wk, wv = oracle.merge("u32", a, b, av, bv)
+    assert np.array_equal(gk, wk) and np.array_equal(gv, wv)
+    a64, b64 = a.astype(np.uint64) * np.uint64(1 << 33), b.astype(np.uint64) * np.uint64(1 << 33)
+    for op in ("union", "intersection", "difference", "symmetric_difference"):
+        assert np.array_equal(oracle.std_set_op_u64(op, a64, b64),
+                              oracle.set_op(op, "u64", a64, b64))
 
 
 def _reference_rows(arity, n):

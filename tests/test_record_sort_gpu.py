@@ -218,6 +218,34 @@ def test_radix_rows_out_of_place_payloads_in_place(ex):
     np.testing.assert_array_equal(d_in.to_host_vec(), rows)
 
 
+@pytest.mark.parametrize("arity", [2, 5])
+@pytest.mark.parametrize("alias", ["payloads", "rows"])
+def test_radix_all_rows_equal_mixed_aliasing(ex, arity, alias):
+    """Every row equal (no pass moves anything) with only one stream in
+    place: the other stream's output must still be written, and the aliased
+    one left intact."""
+    from rccl_amd import _abi
+
+    n = RADIX_MIN_ROWS * 2 + 5
+    rows = np.full((n, arity), 0x01020304, dtype=np.uint32)
+    pay = workloads.hash_range(91 + arity, n)
+    d_in = rs.RowBuffer.from_host(rows)
+    d_pay_in = DeviceBuffer.from_host(pay)
+    if alias == "payloads":
+        d_out, d_pay_out = rs.RowBuffer.zeroed(arity, n), d_pay_in
+    else:
+        d_out, d_pay_out = d_in, DeviceBuffer.from_host(np.zeros(n, np.uint64))
+    ws_bytes = _abi.workspace_bytes("rccl_hip_record_sort_workspace_bytes", arity, 8, n)
+    ws = DeviceBuffer.bytes(ws_bytes)
+    launch = ex.launch()
+    _abi.check(_abi.load().rccl_hip_record_sort(arity, 8, d_in.ptr, d_pay_in.ptr, d_out.ptr,
+                                                d_pay_out.ptr, n, ws.ptr, ws_bytes,
+                                                launch.handle))
+    ex.synchronize()
+    np.testing.assert_array_equal(d_out.to_host_vec(), rows)
+    np.testing.assert_array_equal(d_pay_out.to_host_vec(), pay)
+
+
 def test_radix_many_tiles_and_groups(ex):
     """2^22 rows of arity 2 (512 tiles, 32 look-back groups per pass), small
     interned ids in the first column and full-range ids in the second."""
