@@ -184,6 +184,28 @@ RCCL_HIP_API rccl_hip_status rccl_hip_radix_sort_buffer(rccl_hip_key_kind key, s
                                            uint32_t end_bit, void *workspace,
                                            size_t workspace_bytes, hipStream_t stream);
 
+/* Size of the device-resident control workspace of rccl_hip_radix_sort_static
+ * (per device, held until the process ends): 48 MiB, enough for 2^28 u32 keys
+ * or 2^28 u64-key/u32-value pairs. */
+#define RCCL_HIP_STATIC_RADIX_WORKSPACE_BYTES (48u << 20)
+
+/* rccl_hip_radix_sort without a workspace argument: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * bins and look-back buffers live in a library-owned static device array of
+ * RCCL_HIP_STATIC_RADIX_WORKSPACE_BYTES per device, and nothing is
+ * allocated. The caller still passes keys, values and the n-item scratch
+ * buffers. A sort whose workspace (rccl_hip_radix_sort_workspace_bytes)
+ * exceeds that size returns RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL before any
+ * launch. Every call on one device shares that device's array (each call
+ * clears what it uses), so calls that overlap on one device (different
+ * streams, or threads) race: serialize them. */
+RCCL_HIP_API rccl_hip_status rccl_hip_radix_sort_static(rccl_hip_key_kind key,
+                                                        size_t value_bytes, rccl_hip_order order,
+                                                        void *keys, void *values,
+                                                        void *scratch_keys, void *scratch_values,
+                                                        size_t n, hipStream_t stream);
+
 /* In-place radix sort of all key bits with caller-owned scratch of n keys
  * (and n values). Replaces device_radix_sort_{keys,pairs}{,_descending}
  * (rccl-cub/src/radix.rs:558-623, :763-876): the result is copied back when

@@ -51,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "rccl_hip_radix_sort_workspace_bytes",
     "rccl_hip_radix_sort_buffer",
     "rccl_hip_radix_sort",
+    "rccl_hip_radix_sort_static",
     "rccl_hip_merge_workspace_bytes",
     "rccl_hip_merge",
     "rccl_hip_merge_sort_workspace_bytes",
@@ -155,6 +156,8 @@ def _declare(lib):
                                                c.c_uint32, c.c_uint32, vp, sz, vp]
     lib_view.rccl_hip_radix_sort.restype = st
     lib_view.rccl_hip_radix_sort.argtypes = [st, sz, st, vp, vp, vp, vp, sz, vp, sz, vp]
+    lib_view.rccl_hip_radix_sort_static.restype = st
+    lib_view.rccl_hip_radix_sort_static.argtypes = [st, sz, st, vp, vp, vp, vp, sz, vp]
     lib_view.rccl_hip_merge_workspace_bytes.restype = st
     lib_view.rccl_hip_merge_workspace_bytes.argtypes = [st, sz, sz, sz, c.POINTER(sz)]
     lib_view.rccl_hip_merge.restype = st

@@ -9,6 +9,7 @@
 namespace rccl_hip {
 namespace radix {
 rccl_hip_status check_lane_order();
+rccl_hip_status static_workspace(void **out);
 } // namespace radix
 } // namespace rccl_hip
 
@@ -188,7 +189,11 @@ rccl_hip_status rccl_hip_program_load(int device) {
   err = hipGetDevice(&current);
   if (err == hipSuccess) err = hipSetDevice(device);
   if (err != hipSuccess) return rccl_hip::set_hip_error(RCCL_HIP_ERROR_DRIVER, "set device", err);
-  const rccl_hip_status st = rccl_hip::radix::check_lane_order();
+  rccl_hip_status st = rccl_hip::radix::check_lane_order();
+  // The static radix workspace's device address, looked up with the device
+  // current (rccl_hip_radix_sort_static).
+  void *static_ws = nullptr;
+  if (st == RCCL_HIP_SUCCESS) st = rccl_hip::radix::static_workspace(&static_ws);
   err = hipSetDevice(current);
   if (st != RCCL_HIP_SUCCESS) return st;
   if (err != hipSuccess) return rccl_hip::set_hip_error(RCCL_HIP_ERROR_DRIVER, "set device", err);

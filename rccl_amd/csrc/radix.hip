@@ -2,10 +2,47 @@
 // ABI (rccl-cub/src/radix.rs:364-876 behaviour). Kernels and pass control are
 // in radix_kernels.hpp; each key kind is instantiated in its own
 // radix_<kind>.hip.
+#include <mutex>
+#include <utility>
+#include <vector>
+
 #include "radix_kernels.hpp"
+
+// Control workspace (bins and the two look-back buffers) of
+// rccl_hip_radix_sort_static: one copy per device, held until the process
+// ends. Host code never uses this name as an address: the device address
+// comes from hipGetSymbolAddress (static_workspace below).
+static __device__ __align__(256) unsigned char scratch[RCCL_HIP_STATIC_RADIX_WORKSPACE_BYTES];
 
 namespace rccl_hip {
 namespace radix {
+
+namespace {
+std::mutex g_static_mu;
+std::vector<std::pair<int, void *>> g_static_ptr;  // (device, device address of scratch)
+} // namespace
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+rccl_hip_status static_workspace(void **out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "current device", err);
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  for (const auto &e : g_static_ptr) {
+    if (e.first == dev) {
+      *out = e.second;
+      return ok();
+    }
+  }
+  void *ptr = nullptr;
+  err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (err != hipSuccess || !ptr)
+    return set_hip_error(RCCL_HIP_ERROR_DRIVER, "static radix workspace address", err);
+  g_static_ptr.emplace_back(dev, ptr);
+  *out = ptr;
+  return ok();
+}
 
 Layout layout(size_t key_bytes, size_t value_bytes, size_t n) {
   Layout l;
@@ -247,6 +284,26 @@ rccl_hip_status rccl_hip_radix_sort_buffer(rccl_hip_key_kind key, size_t value_b
   }
   *current_is_first = a.cur == 0 ? 1 : 0;
   return ok();
+}
+
+rccl_hip_status rccl_hip_radix_sort_static(rccl_hip_key_kind key, size_t value_bytes,
+                                           rccl_hip_order order, void *keys, void *values,
+                                           void *scratch_keys, void *scratch_values, size_t n,
+                                           hipStream_t stream) {
+  if (!radix::radix_kind(key)) return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix key kind");
+  if (!valid_value_bytes(value_bytes))
+    return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix value bytes");
+  if (n > radix::MAX_ITEMS)
+    return set_error(RCCL_HIP_ERROR_LENGTH_MISMATCH, "radix item count", radix::MAX_ITEMS, n);
+  const size_t need = radix::layout(key_bytes(key), value_bytes, n).total;
+  if (need > RCCL_HIP_STATIC_RADIX_WORKSPACE_BYTES)
+    return set_error(RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL, "static radix workspace", need,
+                     RCCL_HIP_STATIC_RADIX_WORKSPACE_BYTES);
+  if (n == 0) return ok();
+  void *ws = nullptr;
+  RCCL_HIP_TRY(radix::static_workspace(&ws));
+  return rccl_hip_radix_sort(key, value_bytes, order, keys, values, scratch_keys, scratch_values,
+                             n, ws, RCCL_HIP_STATIC_RADIX_WORKSPACE_BYTES, stream);
 }
 
 rccl_hip_status rccl_hip_radix_sort(rccl_hip_key_kind key, size_t value_bytes,

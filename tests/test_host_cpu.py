@@ -415,3 +415,21 @@ def test_comparator_classification():
     with pytest.raises(ValueError):
         cub.order_code(7)
 
+
+def test_static_radix_rejects_oversized_before_any_launch(lib):
+    """rccl_hip_radix_sort_static refuses a sort whose control workspace
+    exceeds its static array (48 MiB) with WorkspaceTooSmall before touching
+    the device; the error names the need and the limit."""
+    limit = 48 << 20
+    n = 1 << 31
+    need = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", _abi.KEY_KINDS["u32"], 0, n)
+    assert need > limit
+    st = lib.rccl_hip_radix_sort_static(_abi.KEY_KINDS["u32"], 0, 0, None, None, None, None, n,
+                                        None)
+    assert st == 2  # WorkspaceTooSmall
+    info = _abi.ErrorInfo()
+    lib.rccl_hip_last_error(ctypes.byref(info))
+    assert (info.expected, info.actual) == (need, limit)
+    assert info.role == b"static radix workspace"
+    assert lib.rccl_hip_radix_sort_static(_abi.KEY_KINDS["u32"], 3, 0, None, None, None, None, 5,
+                                          None) == 9  # InvalidArgument
