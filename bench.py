@@ -682,6 +682,10 @@ def main():
     ap.add_argument("--no-ordering", action="store_true",
                     help="skip the C4 merge / merge sort and C5 set operation legs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ranking", choices=("auto", "lane_atomic", "match_any"), default="auto",
+                    help="onesweep ranking mode (rccl_hip_radix_configure)")
+    ap.add_argument("--tile-order", choices=("auto", "ticket"), default="auto",
+                    help="onesweep tile order (rccl_hip_radix_configure)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -699,6 +703,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    cub.Program.load(0)
+    abi.check(abi.load().rccl_hip_radix_configure(abi.RANKING[args.ranking],
+                                                  abi.TILE_ORDER[args.tile_order]))
     n = 1 << args.log2n
     _log(f"u32 keys n=2^{args.log2n}")
     keys_t = wd.metric_u32_keys(n)
@@ -744,6 +751,7 @@ def main():
                              "radix_onesweep (one 8-bit pass: 4n read + 4n write)",
                              profiled_traffic("radix_onesweep_u32", args.log2n)),
         "kernel_ms": _rounded(r32["kernel_ms"]),
+        "radix_modes": {"ranking": args.ranking, "tile_order": args.tile_order},
         "validated": r32["validated"],
     }
     valid = r32["validated"]

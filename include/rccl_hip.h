@@ -184,6 +184,33 @@ RCCL_HIP_API rccl_hip_status rccl_hip_radix_sort_buffer(rccl_hip_key_kind key, s
                                            uint32_t end_bit, void *workspace,
                                            size_t workspace_bytes, hipStream_t stream);
 
+/* Onesweep ranking modes (rccl_hip_radix_configure). */
+enum {
+  RCCL_HIP_RANKING_AUTO = 0,        /* lane-ordered atomics where the device check passes,
+                                       else match-any */
+  RCCL_HIP_RANKING_LANE_ATOMIC = 1, /* returning LDS atomics served in lane order */
+  RCCL_HIP_RANKING_MATCH_ANY = 2    /* wave64 ballot/mbcnt match-any multisplit */
+};
+
+/* Onesweep tile orders (rccl_hip_radix_configure). */
+enum {
+  RCCL_HIP_TILE_ORDER_AUTO = 0,  /* XCD-ordered tiles where the device check sees blocks land
+                                    on the 8 XCDs round-robin, else tickets */
+  RCCL_HIP_TILE_ORDER_TICKET = 1 /* every block claims its tile from an atomic ticket */
+};
+
+/* Selects how the radix sort ranks keys within a tile and how blocks find
+ * their tiles, for every later call in the process (every radix path: radix
+ * sort, the merge-sort lowering and the record sort). No counterpart in the
+ * reference, whose onesweep always ranks with match-any and claims tiles
+ * from a ticket (rccl-cub/src/ordering_backend/radix.rs:918-938, :1078-1087).
+ * The output is identical in every mode; the defaults are the fastest ones
+ * the device supports. RCCL_HIP_RANKING_LANE_ATOMIC makes sorts return
+ * RCCL_HIP_ERROR_UNSUPPORTED_TARGET on a device whose LDS does not serve
+ * same-address atomic lanes in lane order (checked once per device by
+ * rccl_hip_program_load). */
+RCCL_HIP_API rccl_hip_status rccl_hip_radix_configure(int ranking, int tile_order);
+
 /* Size of the device-resident control workspace of rccl_hip_radix_sort_static
  * (per device, held until the process ends): 48 MiB, enough for 2^28 u32 keys
  * or 2^28 u64-key/u32-value pairs. */

@@ -36,6 +36,8 @@ KEY_KINDS = {
 RADIX_KINDS = ("u32", "i32", "f32", "u64", "i64", "f64")
 ASCENDING = 0
 DESCENDING = 1
+RANKING = {"auto": 0, "lane_atomic": 1, "match_any": 2}
+TILE_ORDER = {"auto": 0, "ticket": 1}
 SET_OPS = {"union": 0, "intersection": 1, "difference": 2, "symmetric_difference": 3}
 GROUP_UNIQUE = 0
 GROUP_OPS = {"natural_bag_add": 1, "boolean_or": 2, "independent_probability_or": 3}
@@ -52,6 +54,7 @@ EXPORTED_SYMBOLS = (
     "rccl_hip_radix_sort_buffer",
     "rccl_hip_radix_sort",
     "rccl_hip_radix_sort_static",
+    "rccl_hip_radix_configure",
     "rccl_hip_merge_workspace_bytes",
     "rccl_hip_merge",
     "rccl_hip_merge_sort_workspace_bytes",
@@ -156,6 +159,8 @@ def _declare(lib):
                                                c.c_uint32, c.c_uint32, vp, sz, vp]
     lib_view.rccl_hip_radix_sort.restype = st
     lib_view.rccl_hip_radix_sort.argtypes = [st, sz, st, vp, vp, vp, vp, sz, vp, sz, vp]
+    lib_view.rccl_hip_radix_configure.restype = st
+    lib_view.rccl_hip_radix_configure.argtypes = [c.c_int, c.c_int]
     lib_view.rccl_hip_radix_sort_static.restype = st
     lib_view.rccl_hip_radix_sort_static.argtypes = [st, sz, st, vp, vp, vp, vp, sz, vp]
     lib_view.rccl_hip_merge_workspace_bytes.restype = st

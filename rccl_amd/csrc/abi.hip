@@ -8,8 +8,9 @@
 
 namespace rccl_hip {
 namespace radix {
-rccl_hip_status check_lane_order();
+struct DeviceCaps;
 rccl_hip_status static_workspace(void **out);
+rccl_hip_status probe_current_device();
 } // namespace radix
 } // namespace rccl_hip
 
@@ -178,8 +179,8 @@ rccl_hip_status rccl_hip_program_load(int device) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0 ||
       (prop.gcnArchName[6] != '\0' && prop.gcnArchName[6] != ':'))
     return rccl_hip::set_error(RCCL_HIP_ERROR_UNSUPPORTED_TARGET, "gfx950 kernels");
-  // The radix ranking relies on lane-ordered LDS atomics: verify once per
-  // device, on that device.
+  // Once per device, on that device: probe the LDS lane order and the XCD
+  // placement the radix sort relies on, and find the static workspace.
   static std::mutex mu;
   static std::vector<int> checked;
   std::lock_guard<std::mutex> lock(mu);
@@ -189,7 +190,7 @@ rccl_hip_status rccl_hip_program_load(int device) {
   err = hipGetDevice(&current);
   if (err == hipSuccess) err = hipSetDevice(device);
   if (err != hipSuccess) return rccl_hip::set_hip_error(RCCL_HIP_ERROR_DRIVER, "set device", err);
-  rccl_hip_status st = rccl_hip::radix::check_lane_order();
+  rccl_hip_status st = rccl_hip::radix::probe_current_device();
   // The static radix workspace's device address, looked up with the device
   // current (rccl_hip_radix_sort_static).
   void *static_ws = nullptr;

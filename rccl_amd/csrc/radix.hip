@@ -2,6 +2,7 @@
 // ABI (rccl-cub/src/radix.rs:364-876 behaviour). Kernels and pass control are
 // in radix_kernels.hpp; each key kind is instantiated in its own
 // radix_<kind>.hip.
+#include <atomic>
 #include <mutex>
 #include <utility>
 #include <vector>
@@ -56,7 +57,8 @@ Layout layout(size_t key_bytes, size_t value_bytes, size_t n) {
   l.groups = (l.tiles + GROUP - 1) / GROUP;
   l.lb_ginc = align_up(l.tiles * BINS * l.desc_bytes, 256);
   l.lb_gagg = l.lb_ginc + align_up(l.groups * BINS * l.desc_bytes, 256);
-  l.lb_bytes = l.lb_gagg + align_up(l.groups * BINS * sizeof(uint32_t), 256);
+  l.lb_ticket = l.lb_gagg + align_up(l.groups * BINS * sizeof(uint32_t), 256);
+  l.lb_bytes = l.lb_ticket + align_up(XCDS * sizeof(uint32_t), 256);
   l.lb[0] = off;
   off += l.lb_bytes;
   l.lb[1] = off;
@@ -67,16 +69,22 @@ Layout layout(size_t key_bytes, size_t value_bytes, size_t n) {
 
 namespace {
 
+// Outputs of the one-time device probes below (no allocation needed).
+constexpr int XCC_PROBE_BLOCKS = 256;
+__device__ uint32_t probe_out[1 + XCC_PROBE_BLOCKS];
+
 // Lane-order self-check (see the onesweep notes): each wave repeatedly adds 1
 // to per-wave LDS counters chosen by a hash of (round, lane) restricted to
 // 1, 2, 16 or 256 counters, and checks that lanes hitting the same counter
 // received consecutive values in lane order. One block of CHECK_THREADS;
-// violations are counted into *bad.
+// the number of violations is written to *bad.
 constexpr int CHECK_THREADS = 256;
 __global__ void __launch_bounds__(CHECK_THREADS) lane_order_check_kernel(uint32_t *bad) {
   __shared__ uint32_t c[CHECK_THREADS / 64][BINS];
+  __shared__ uint32_t total;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   for (uint32_t i = tid; i < (CHECK_THREADS / 64) * BINS; i += CHECK_THREADS) (&c[0][0])[i] = 0;
+  if (tid == 0) total = 0;
   __syncthreads();
   uint32_t nbad = 0;
   for (uint32_t round = 0; round < 64; ++round) {
@@ -101,27 +109,88 @@ __global__ void __launch_bounds__(CHECK_THREADS) lane_order_check_kernel(uint32_
     nbad += static_cast<uint32_t>(__shfl(static_cast<int>(base), static_cast<int>(first), 64)) !=
             base;
   }
-  if (nbad) atomicAdd(bad, nbad);
+  if (nbad) atomicAdd(&total, nbad);
+  __syncthreads();
+  if (tid == 0) *bad = total;
+}
+
+// Where blocks land: block b records its XCD (HW_REG_XCC_ID, all 4 bits).
+__global__ void __launch_bounds__(64) xcc_probe_kernel(uint32_t *out) {
+  if (threadIdx.x == 0)
+    out[blockIdx.x] = static_cast<uint32_t>(__builtin_amdgcn_s_getreg((3 << 11) | 20));
+}
+
+// Modes requested with rccl_hip_radix_configure (RCCL_HIP_RANKING_*,
+// RCCL_HIP_TILE_ORDER_*).
+std::atomic<int> g_ranking{0};
+std::atomic<int> g_tile_order{0};
+
+struct CapsEntry {
+  int device;
+  DeviceCaps caps;
+};
+std::mutex g_caps_mu;
+std::vector<CapsEntry> g_caps;
+
+rccl_hip_status probe_device(DeviceCaps *caps) {
+  uint32_t *out = nullptr;
+  hipError_t err = hipGetSymbolAddress(reinterpret_cast<void **>(&out), HIP_SYMBOL(probe_out));
+  uint32_t host[1 + XCC_PROBE_BLOCKS] = {};
+  if (err == hipSuccess) {
+    lane_order_check_kernel<<<1, CHECK_THREADS>>>(out);
+    xcc_probe_kernel<<<XCC_PROBE_BLOCKS, 64>>>(out + 1);
+    err = hipGetLastError();
+  }
+  if (err == hipSuccess) err = hipMemcpy(host, out, sizeof(host), hipMemcpyDeviceToHost);
+  if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "radix device probe", err);
+  caps->lane_order = host[0] == 0;
+  bool round_robin = true;
+  for (int b = 0; b < XCC_PROBE_BLOCKS; ++b) round_robin &= host[1 + b] == uint32_t(b) % XCDS;
+  caps->nx = round_robin ? XCDS : 1u;
+  caps->rank = caps->lane_order ? Rank::LaneAtomic : Rank::MatchAny;
+  return ok();
 }
 
 } // namespace
 
-rccl_hip_status check_lane_order() {
-  uint32_t *bad = nullptr;
-  hipError_t err = hipMalloc(&bad, sizeof(uint32_t));
-  if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_MEMORY, "lane-order check", err);
-  uint32_t host = 0;
-  err = hipMemset(bad, 0, sizeof(uint32_t));
-  if (err == hipSuccess) {
-    lane_order_check_kernel<<<1, CHECK_THREADS>>>(bad);
-    err = hipGetLastError();
+namespace {
+// The current device's probed caps, probing it on first use.
+rccl_hip_status probed_caps(DeviceCaps *caps) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "current device", err);
+  std::lock_guard<std::mutex> lock(g_caps_mu);
+  for (const CapsEntry &e : g_caps) {
+    if (e.device == dev) {
+      *caps = e.caps;
+      return ok();
+    }
   }
-  if (err == hipSuccess) err = hipMemcpy(&host, bad, sizeof(uint32_t), hipMemcpyDeviceToHost);
-  const hipError_t free_err = hipFree(bad);
-  if (err == hipSuccess) err = free_err;
-  if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "lane-order check", err);
-  if (host != 0)
-    return set_error(RCCL_HIP_ERROR_UNSUPPORTED_TARGET, "lane-ordered LDS atomics", 0, host);
+  RCCL_HIP_TRY(probe_device(caps));
+  g_caps.push_back(CapsEntry{dev, *caps});
+  return ok();
+}
+} // namespace
+
+rccl_hip_status probe_current_device() {
+  DeviceCaps caps;
+  return probed_caps(&caps);
+}
+
+rccl_hip_status device_caps(DeviceCaps *caps) {
+  DeviceCaps c;
+  RCCL_HIP_TRY(probed_caps(&c));
+  switch (g_ranking.load(std::memory_order_relaxed)) {
+  case RCCL_HIP_RANKING_LANE_ATOMIC:
+    if (!c.lane_order)
+      return set_error(RCCL_HIP_ERROR_UNSUPPORTED_TARGET, "lane-ordered LDS atomics");
+    c.rank = Rank::LaneAtomic;
+    break;
+  case RCCL_HIP_RANKING_MATCH_ANY: c.rank = Rank::MatchAny; break;
+  default: break;
+  }
+  if (g_tile_order.load(std::memory_order_relaxed) == RCCL_HIP_TILE_ORDER_TICKET) c.nx = 1;
+  *caps = c;
   return ok();
 }
 
@@ -235,6 +304,17 @@ rccl_hip_status merge_sort_lowering(rccl_hip_key_kind key, size_t value_bytes, b
 using namespace rccl_hip;
 
 extern "C" {
+
+rccl_hip_status rccl_hip_radix_configure(int ranking, int tile_order) {
+  if (ranking != RCCL_HIP_RANKING_AUTO && ranking != RCCL_HIP_RANKING_LANE_ATOMIC &&
+      ranking != RCCL_HIP_RANKING_MATCH_ANY)
+    return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix ranking mode");
+  if (tile_order != RCCL_HIP_TILE_ORDER_AUTO && tile_order != RCCL_HIP_TILE_ORDER_TICKET)
+    return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix tile order");
+  radix::g_ranking.store(ranking);
+  radix::g_tile_order.store(tile_order);
+  return ok();
+}
 
 rccl_hip_status rccl_hip_radix_sort_workspace_bytes(rccl_hip_key_kind key, size_t value_bytes,
                                                     size_t n, size_t *bytes) {

@@ -208,20 +208,21 @@ struct RowBuffers {
   Val *vout, *vscratch;
 };
 
-template <int N, class Val, int ITEMS>
+template <int N, class Val, int ITEMS, radix::Rank RANK>
 __global__ void __launch_bounds__(RADIX_THREADS, RCCL_RADIX_WAVES_PER_SIMD)
 row_onesweep_kernel(RowBuffers<N, Val> b, size_t n, uint32_t num_tiles,
                     const uint32_t *__restrict__ pass_bins, const PassPlan *__restrict__ plan,
-                    LookbackBuf<uint32_t> lb0, LookbackBuf<uint32_t> lb1, uint32_t bit) {
+                    LookbackBuf<uint32_t> lb0, LookbackBuf<uint32_t> lb1, uint32_t nx,
+                    uint32_t bit) {
   const PassPlan pl = *plan;
   if (!pl.active) return;
   const Row<N> *kin = pl.src == 0 ? b.in : (pl.src == 1 ? b.out : b.scratch);
   Row<N> *kout = pl.dst == 1 ? b.out : b.scratch;
   const Val *vin = pl.src == 0 ? b.vin : (pl.src == 1 ? b.vout : b.vscratch);
   Val *vout = pl.dst == 1 ? b.vout : b.vscratch;
-  radix::onesweep_tile<Row<N>, Val, RowDigits<N>, ITEMS, uint32_t, RADIX_THREADS>(
-      kin, kout, vin, vout, n, num_tiles, pass_bins, pl.lb ? lb1 : lb0, pl.lb ? lb0 : lb1, bit,
-      0xFFu);
+  radix::onesweep_tile<Row<N>, Val, RowDigits<N>, ITEMS, uint32_t, RADIX_THREADS, RANK>(
+      kin, kout, vin, vout, n, num_tiles, pass_bins, pl.lb ? lb1 : lb0, pl.lb ? lb0 : lb1, nx,
+      bit, 0xFFu);
 }
 
 // ---------------------------------------------------------------------------
@@ -231,7 +232,7 @@ struct RadixLayout {
   size_t tiles = 0, groups = 0;
   size_t bins = 0, plan = 0;
   size_t lb[2] = {0, 0};
-  size_t lb_ginc = 0, lb_gagg = 0, lb_bytes = 0;
+  size_t lb_ginc = 0, lb_gagg = 0, lb_ticket = 0, lb_bytes = 0;
   size_t scratch_rows = 0, scratch_vals = 0;
   size_t total = 0;
 };
@@ -251,7 +252,8 @@ RadixLayout radix_layout(size_t n) {
   off += align_up(P * sizeof(PassPlan), 256);
   l.lb_ginc = align_up(l.tiles * BINS * sizeof(uint32_t), 256);
   l.lb_gagg = l.lb_ginc + align_up(l.groups * BINS * sizeof(uint32_t), 256);
-  l.lb_bytes = l.lb_gagg + align_up(l.groups * BINS * sizeof(uint32_t), 256);
+  l.lb_ticket = l.lb_gagg + align_up(l.groups * BINS * sizeof(uint32_t), 256);
+  l.lb_bytes = l.lb_ticket + align_up(XCDS * sizeof(uint32_t), 256);
   l.lb[0] = off;
   off += l.lb_bytes;
   l.lb[1] = off;
@@ -273,9 +275,36 @@ struct RecordArgs {
   hipStream_t stream;
 };
 
+// The 4N onesweep launches of a row sort, in one ranking mode.
+template <int N, class Val, radix::Rank RANK>
+rccl_hip_status launch_row_onesweeps(const RecordArgs &a, const RadixLayout &l,
+                                     const RowBuffers<N, Val> &b, const uint32_t *bins,
+                                     const PassPlan *plan, const LookbackBuf<uint32_t> (&lb)[2],
+                                     uint32_t nx) {
+  constexpr int ITEMS = radix_items<N, Val>();
+  constexpr uint32_t P = 4 * N;
+  size_t resident = 0;
+  RCCL_HIP_TRY(resident_blocks(
+      reinterpret_cast<const void *>(&row_onesweep_kernel<N, Val, ITEMS, RANK>), RADIX_THREADS,
+      &resident));
+  // The XCD order needs two rows of runs resident at once; with fewer, blocks
+  // claim ticketed tiles instead.
+  if (nx == XCDS && resident < 2 * size_t(XCDS) * radix::XCD_RUN) nx = 1;
+  const uint32_t grid = static_cast<uint32_t>(radix::onesweep_grid(l.tiles, nx));
+  for (uint32_t p = 0; p < P; ++p) {
+    const uint32_t word = uint32_t(N) - 1u - p / 4u;
+    const uint32_t bit = 32u * word + 8u * (p % 4u);
+    KernelTimer t("record_onesweep", a.stream, a.n);
+    row_onesweep_kernel<N, Val, ITEMS, RANK><<<dim3(grid), RADIX_THREADS, 0, a.stream>>>(
+        b, a.n, static_cast<uint32_t>(l.tiles), bins + size_t(p) * BINS, plan + p, lb[0], lb[1],
+        nx, bit);
+    RCCL_HIP_TRY(check_launch("record sort onesweep"));
+  }
+  return ok();
+}
+
 template <int N, class Val>
 rccl_hip_status run_radix(const RecordArgs &a) {
-  constexpr int ITEMS = radix_items<N, Val>();
   constexpr uint32_t P = 4 * N;
   const RadixLayout l = radix_layout<N, Val>(a.n);
   if (!a.ws || a.ws_bytes < l.total)
@@ -290,6 +319,7 @@ rccl_hip_status run_radix(const RecordArgs &a) {
     lb[i].tile = reinterpret_cast<uint32_t *>(base);
     lb[i].ginc = reinterpret_cast<uint32_t *>(base + l.lb_ginc);
     lb[i].gagg = reinterpret_cast<uint32_t *>(base + l.lb_gagg);
+    lb[i].ticket = reinterpret_cast<uint32_t *>(base + l.lb_ticket);
   }
   RowBuffers<N, Val> b;
   b.in = static_cast<const Row<N> *>(a.in);
@@ -299,21 +329,16 @@ rccl_hip_status run_radix(const RecordArgs &a) {
   b.vout = static_cast<Val *>(a.out_v);
   b.vscratch = reinterpret_cast<Val *>(ws + l.scratch_vals);
 
-  static int cus = 0, blocks_per_cu = 0;
-  if (cus == 0 || blocks_per_cu == 0) {
+  radix::DeviceCaps caps;
+  RCCL_HIP_TRY(radix::device_caps(&caps));
+  static int cus = 0;
+  if (cus == 0) {
     int dev = 0;
     hipError_t err = hipGetDevice(&dev);
     if (err == hipSuccess)
       err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (err == hipSuccess)
-      err = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &blocks_per_cu, row_onesweep_kernel<N, Val, ITEMS>, RADIX_THREADS, 0);
     if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "record sort device", err);
   }
-  // The XCD-aware tile order needs the blocks of one row of runs (and the
-  // next) resident at once.
-  if (size_t(blocks_per_cu) * size_t(cus) < 2 * size_t(XCDS) * radix::XCD_RUN)
-    return set_error(RCCL_HIP_ERROR_LAUNCH, "record radix onesweep does not fit on the device");
 
   {
     KernelTimer t("record_init", a.stream, 0);
@@ -337,17 +362,11 @@ rccl_hip_status run_radix(const RecordArgs &a) {
         l.lb_bytes / sizeof(uint32_t));
   }
   RCCL_HIP_TRY(check_launch("record sort histogram"));
-  const uint32_t grid = static_cast<uint32_t>(radix::onesweep_grid(l.tiles));
-  for (uint32_t p = 0; p < P; ++p) {
-    const uint32_t word = uint32_t(N) - 1u - p / 4u;
-    const uint32_t bit = 32u * word + 8u * (p % 4u);
-    KernelTimer t("record_onesweep", a.stream, a.n);
-    row_onesweep_kernel<N, Val, ITEMS><<<dim3(grid), RADIX_THREADS, 0, a.stream>>>(
-        b, a.n, static_cast<uint32_t>(l.tiles), bins + size_t(p) * BINS, plan + p, lb[0], lb[1],
-        bit);
-    RCCL_HIP_TRY(check_launch("record sort onesweep"));
-  }
-  return ok();
+  return caps.rank == radix::Rank::LaneAtomic
+             ? launch_row_onesweeps<N, Val, radix::Rank::LaneAtomic>(a, l, b, bins, plan, lb,
+                                                                     caps.nx)
+             : launch_row_onesweeps<N, Val, radix::Rank::MatchAny>(a, l, b, bins, plan, lb,
+                                                                   caps.nx);
 }
 
 } // namespace record_sort

@@ -37,3 +37,19 @@ def launch():
 
     program = cub.Program.load(0)
     return program.on(torch.cuda.current_stream(0))
+
+
+@pytest.fixture(params=["default", "match_any", "ticket_tiles"])
+def radix_ranking(request, launch):
+    """Runs a radix test under the device's default onesweep (lane-ordered LDS
+    atomics, XCD-ordered tiles on gfx950), under wave64 ballot match-any
+    ranking, and with every block claiming its tile from an atomic ticket.
+    The output must be identical."""
+    from rccl_amd import _abi
+
+    lib = _abi.load()
+    ranking = "match_any" if request.param == "match_any" else "auto"
+    order = "ticket" if request.param == "ticket_tiles" else "auto"
+    _abi.check(lib.rccl_hip_radix_configure(_abi.RANKING[ranking], _abi.TILE_ORDER[order]))
+    yield request.param
+    _abi.check(lib.rccl_hip_radix_configure(0, 0))

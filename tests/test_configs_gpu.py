@@ -32,7 +32,7 @@ from rccl_amd import cub, workloads
 from rccl_amd import workloads_device as wd
 from rccl_amd.device import DeviceBuffer
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("radix_ranking")]
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.json")
 NP = {"u32": np.uint32, "i32": np.int32, "f32": np.float32, "u64": np.uint64,

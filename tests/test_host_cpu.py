@@ -433,3 +433,14 @@ def test_static_radix_rejects_oversized_before_any_launch(lib):
     assert info.role == b"static radix workspace"
     assert lib.rccl_hip_radix_sort_static(_abi.KEY_KINDS["u32"], 3, 0, None, None, None, None, 5,
                                           None) == 9  # InvalidArgument
+
+
+def test_radix_configure_validates(lib):
+    """The diagnostic mode switch accepts the documented modes only."""
+    assert lib.rccl_hip_radix_configure(3, 0) == 9  # InvalidArgument
+    assert lib.rccl_hip_radix_configure(0, 2) == 9
+    assert lib.rccl_hip_radix_configure(-1, 0) == 9
+    for ranking in _abi.RANKING.values():
+        for order in _abi.TILE_ORDER.values():
+            assert lib.rccl_hip_radix_configure(ranking, order) == 0
+    assert lib.rccl_hip_radix_configure(0, 0) == 0

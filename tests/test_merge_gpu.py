@@ -245,7 +245,7 @@ def test_merge_sort_c4_scaled(launch):
 
 
 @pytest.mark.parametrize("kind", ["u32", "i32", "u64", "i64"])
-def test_merge_sort_radix_lowering(launch, kind):
+def test_merge_sort_radix_lowering(launch, radix_ranking, kind):
     """From 65,536 items, integer keys sort through the stable radix lowering.
     Sizes on both sides of that threshold, ties (stability, with payloads
     recording the input order), both orders, in-place and copy forms."""
@@ -277,7 +277,7 @@ def test_merge_sort_radix_lowering(launch, kind):
                     assert v.to_host_vec().tobytes() == vals.tobytes(), "input modified"
 
 
-def test_merge_sort_c4_full_size(launch):
+def test_merge_sort_c4_full_size(launch, radix_ranking):
     """The benchmark's C4 merge sort (2^26 u32 keys in [0, 2^24), copy form),
     bit-exact with numpy's stable sort (keys only, so any correct sort is the
     stable one)."""
@@ -288,7 +288,7 @@ def test_merge_sort_c4_full_size(launch):
 
 @pytest.mark.parametrize("kind", ["u32", "i64"])
 @pytest.mark.parametrize("shape", ["constant", "low_byte_constant", "top_byte_only"])
-def test_merge_sort_radix_lowering_trivial_passes(launch, kind, shape):
+def test_merge_sort_radix_lowering_trivial_passes(launch, radix_ranking, kind, shape):
     """The radix lowering skips passes whose byte is the same in every key;
     the plan must still leave a stable result in the output, in place (even
     active-pass count) and in the copy form (the input read first): every
@@ -319,7 +319,8 @@ def test_merge_sort_radix_lowering_trivial_passes(launch, kind, shape):
 @pytest.mark.parametrize("kind", ["u32", "u64"])
 @pytest.mark.parametrize("alias", ["keys", "values"])
 @pytest.mark.parametrize("shape", ["one_byte", "constant", "full"])
-def test_merge_sort_radix_lowering_mixed_aliasing(launch, kind, alias, shape):
+def test_merge_sort_radix_lowering_mixed_aliasing(launch, radix_ranking, kind, alias,
+                                                  shape):
     """Above the lowering threshold, keys in place with values copied (or the
     reverse): the plan must not let one pass read and write the in-place
     stream, and must write the copied stream even when no pass is needed."""

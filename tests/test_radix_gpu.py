@@ -12,7 +12,7 @@ import oracle
 from rccl_amd import cub, workloads
 from rccl_amd.device import DeviceBuffer
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("radix_ranking")]
 
 
 def _sort_keys(launch, host, descending=False):

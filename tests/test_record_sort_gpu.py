@@ -19,7 +19,7 @@ from rccl_amd import record_sort as rs
 from rccl_amd import thrust, workloads
 from rccl_amd.device import DeviceBuffer
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("radix_ranking")]
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.json")
 
