@@ -656,17 +656,26 @@ def run_search(torch, np, abi, DeviceBuffer, wd, log2_hay, log2_q, steps, warmup
 
 
 def run_c1_latency(torch, np, cub, abi, DeviceBuffer, wd, steps, warmup):
-    """C1 (2^20 u32 keys, cache-resident): latency of one in-place sort."""
+    """C1 (2^20 u32 keys, cache-resident): latency of one in-place sort; and
+    the single-tile route at its capacity (4,864 u32 keys: one launch)
+    beside one key more (the onesweep route: init, histogram, bins scan and
+    four passes)."""
     n = 1 << 20
     keys_t = wd.c1_keys(n)
     r = run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, None, steps, warmup)
+    small = {}
+    for m in (4864, 4865):
+        rs = run_radix(torch, np, cub, abi, DeviceBuffer, keys_t[:m].clone(), None, steps, warmup)
+        small[str(m)] = {"us_per_sort": round(rs["ms"] * 1e3, 2), "launches": rs["launches"],
+                         "validated": rs["validated"]}
     return {
         "workload": "C1 DeviceRadixSort keys-only, 2^20 u32 uniform keys, ascending "
                     "(cache-resident: latency, roofline informative only)",
         "us_per_sort": round(r["ms"] * 1e3, 2), "us_per_sort_min": round(r["ms_min"] * 1e3, 2),
         "value": round(n / (r["ms"] * 1e-3) / 1e9, 3), "unit": "Gkeys/s",
         "launches": r["launches"], "kernel_ms": _rounded(r["kernel_ms"]),
-        "validated": r["validated"],
+        "single_tile_route": small,
+        "validated": r["validated"] and all(v["validated"] for v in small.values()),
     }
 
 

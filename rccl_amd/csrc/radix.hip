@@ -236,15 +236,6 @@ rccl_hip_status sort_buffer(rccl_hip_key_kind key, size_t value_bytes, rccl_hip_
   return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix key kind");
 }
 
-// Inputs of at most this many items take the reference's single-tile route
-// (rccl-cub/src/workspace.rs:22-66: 256 threads x 19 * 4 / max(item bytes, 4)
-// items), which flips the DoubleBuffer selector once whatever the number of
-// digit passes (rccl-cub/src/radix.rs:470-492).
-size_t single_tile_items(size_t key_bytes_, size_t value_bytes) {
-  const size_t item = std::max<size_t>(std::max(key_bytes_, value_bytes), 4);
-  return 256 * std::max<size_t>(1, 19 * 4 / item);
-}
-
 } // namespace
 
 size_t merge_sort_lowering_bytes(size_t key_bytes_, size_t value_bytes, size_t n) {
@@ -347,21 +338,10 @@ rccl_hip_status rccl_hip_radix_sort_buffer(rccl_hip_key_kind key, size_t value_b
   a.end_bit = end_bit;
   a.ws = static_cast<unsigned char *>(workspace);
   a.stream = stream;
+  // Every onesweep pass flips the selector; the single-tile route (one
+  // launch) flips it once, as the reference's does.
+  a.single_to_other = true;
   RCCL_HIP_TRY(radix::sort_buffer(key, value_bytes, order, a, workspace_bytes));
-  // Every pass flips the selector. Where the reference would have taken its
-  // single-tile route (one flip) and the pass count is even, the result is
-  // moved to the other buffer so the selector matches.
-  const uint32_t passes = (end_bit - begin_bit + 7u) / 8u;
-  if (n && passes % 2 == 0 && passes &&
-      n <= radix::single_tile_items(key_bytes(key), value_bytes)) {
-    hipError_t err = hipMemcpyAsync(a.keys[1 - a.cur], a.keys[a.cur], n * key_bytes(key),
-                                    hipMemcpyDeviceToDevice, stream);
-    if (err == hipSuccess && value_bytes)
-      err = hipMemcpyAsync(a.vals[1 - a.cur], a.vals[a.cur], n * value_bytes,
-                           hipMemcpyDeviceToDevice, stream);
-    if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_MEMORY, "radix selector copy", err);
-    a.cur = 1 - a.cur;
-  }
   *current_is_first = a.cur == 0 ? 1 : 0;
   return ok();
 }

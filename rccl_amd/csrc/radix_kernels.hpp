@@ -880,6 +880,121 @@ planned_onesweep_kernel(PlanBuffers<Bits, Val> b, size_t n, uint32_t num_tiles,
 }
 
 // ---------------------------------------------------------------------------
+// single tile: inputs of at most single_tile_items() items are sorted by one
+// block in one launch (the reference's single-tile route,
+// rccl-cub/src/radix.rs:470-492, ordering_backend/radix.rs:366-715). Keys
+// and values are loaded into LDS once; every 8-bit pass counts, scans and
+// ranks them as a onesweep tile does (per-wave counters, either ranking
+// mode) and scatters them into the other LDS buffer; the result is stored
+// once. No workspace is touched.
+// ---------------------------------------------------------------------------
+constexpr int ST_THREADS = 256;
+
+// The reference's single-tile capacity: 256 threads x 19 * 4 / max(item
+// bytes, 4) items (rccl-cub/src/workspace.rs:22-66).
+constexpr size_t single_tile_items(size_t key_bytes, size_t value_bytes) {
+  const size_t item = std::max<size_t>(std::max(key_bytes, value_bytes), 4);
+  return size_t(ST_THREADS) * std::max<size_t>(1, 19 * 4 / item);
+}
+
+template <class Bits, class Val, class Ops, int ITEMS, Rank RANK>
+__global__ void __launch_bounds__(ST_THREADS)
+single_tile_kernel(const Bits *keys_in, Bits *keys_out, const Val *vals_in, Val *vals_out,
+                   uint32_t n, uint32_t begin_bit, uint32_t end_bit) {
+  // keys_out may be keys_in (in place): every input is read before the first
+  // barrier and every output written after the last.
+  constexpr bool PAIRS = !std::is_same<Val, NoValue>::value;
+  constexpr int WAVES = ST_THREADS / 64;
+  constexpr int TILE = ST_THREADS * ITEMS;
+  constexpr int WAVE_ITEMS = 64 * ITEMS;
+  constexpr int NB = BINS + 1;
+  constexpr uint32_t DUMMY = BINS;
+  static_assert(ST_THREADS == BINS, "one thread per digit");
+  using VStore = typename std::conditional<PAIRS, Val, char>::type;
+  __shared__ Bits kbuf[2][TILE];
+  __shared__ VStore vbuf[PAIRS ? 2 : 1][PAIRS ? TILE : 1];
+  __shared__ uint32_t cnt[WAVES][NB];
+  __shared__ uint32_t wave_sum[WAVES];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  for (uint32_t i = tid; i < n; i += ST_THREADS) {
+    kbuf[0][i] = keys_in[i];
+    if constexpr (PAIRS) vbuf[0][i] = vals_in[i];
+  }
+  int cur = 0;
+  for (uint32_t bit = begin_bit; bit < end_bit; bit += 8) {
+    const uint32_t mask = (1u << min(8u, end_bit - bit)) - 1u;
+    for (uint32_t i = tid; i < WAVES * NB; i += ST_THREADS) (&cnt[0][0])[i] = 0;
+    __syncthreads();
+    // (wave, item, lane) order is source order; items at or past n are
+    // dummies, placed after every key.
+    Bits key[ITEMS];
+    uint32_t dg[ITEMS];
+    uint32_t *wcnt = cnt[wave];
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      const uint32_t i = wave * WAVE_ITEMS + uint32_t(j) * 64 + lane;
+      key[j] = kbuf[cur][min(i, uint32_t(TILE - 1))];
+      dg[j] = i < n ? Ops::digit(key[j], bit, mask) : DUMMY;
+      __hip_atomic_fetch_add(&wcnt[dg[j]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    __syncthreads();
+    // Digit starts (exclusive scan over digits), then each wave's start.
+    uint32_t wc[WAVES], count = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      wc[w] = cnt[w][tid];
+      count += wc[w];
+    }
+    const uint32_t inc = wave_inclusive_sum(count, lane);
+    if (lane == 63) wave_sum[wave] = inc;
+    __syncthreads();
+    uint32_t run = inc - count;
+    for (uint32_t w = 0; w < wave; ++w) run += wave_sum[w];
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      cnt[w][tid] = run;
+      run += wc[w];
+    }
+    if (tid < WAVES) cnt[tid][DUMMY] = max(n, tid * uint32_t(WAVE_ITEMS));
+    __syncthreads();
+    const uint32_t dbits = mask | DUMMY;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      const uint32_t d = dg[j];
+      uint32_t pos;
+      if constexpr (RANK == Rank::MatchAny) {
+        const uint64_t m = peer_lanes(d, dbits);
+        const uint32_t below = popc_below(m);
+        const uint32_t base =
+            below == 0 ? __hip_atomic_fetch_add(&wcnt[d],
+                                                static_cast<uint32_t>(__builtin_popcountll(m)),
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                       : 0u;
+        pos = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(
+                  static_cast<int>(lowest_lane(m) << 2), static_cast<int>(base))) +
+              below;
+      } else {
+        pos = __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+      pos = min(pos, uint32_t(TILE - 1));
+      kbuf[cur ^ 1][pos] = key[j];
+      if constexpr (PAIRS) {
+        const uint32_t i = wave * WAVE_ITEMS + uint32_t(j) * 64 + lane;
+        vbuf[cur ^ 1][pos] = vbuf[cur][min(i, uint32_t(TILE - 1))];
+      }
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+  for (uint32_t i = tid; i < n; i += ST_THREADS) {
+    keys_out[i] = kbuf[cur][i];
+    if constexpr (PAIRS) vals_out[i] = vbuf[cur][i];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
 
@@ -934,6 +1049,10 @@ struct SortArgs {
   // the layout's.
   bool planned = false;
   uint32_t plan_flags = 0;
+  // A single-tile sort (n <= single_tile_items) writes its result into the
+  // other buffer of the pair (the DoubleBuffer form: one selector flip, as
+  // the reference's single-tile route) or back into the current one.
+  bool single_to_other = false;
 };
 
 inline size_t plan_bytes() { return align_up(8 * sizeof(PassPlan), 256); }
@@ -1013,10 +1132,31 @@ rccl_hip_status launch_onesweeps(SortArgs &a, const Layout &l, uint32_t passes,
   return ok();
 }
 
+template <class Bits, class Val, class Ops, Rank RANK>
+rccl_hip_status launch_single_tile(SortArgs &a) {
+  constexpr size_t VBYTES = std::is_same<Val, NoValue>::value ? 0 : sizeof(Val);
+  constexpr int ITEMS = static_cast<int>(single_tile_items(sizeof(Bits), VBYTES) / ST_THREADS);
+  const int dst = a.single_to_other ? 1 - a.cur : a.cur;
+  {
+    KernelTimer t("radix_single_tile", a.stream, a.n);
+    single_tile_kernel<Bits, Val, Ops, ITEMS, RANK><<<1, ST_THREADS, 0, a.stream>>>(
+        static_cast<const Bits *>(a.keys[a.cur]), static_cast<Bits *>(a.keys[dst]),
+        static_cast<const Val *>(a.vals[a.cur]), static_cast<Val *>(a.vals[dst]),
+        static_cast<uint32_t>(a.n), a.begin_bit, a.end_bit);
+  }
+  RCCL_HIP_TRY(check_launch("radix single tile"));
+  a.cur = dst;
+  return ok();
+}
+
 template <class Bits, class Val, class Ops, class Desc>
 rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
   DeviceCaps caps;
   RCCL_HIP_TRY(device_caps(&caps));
+  constexpr size_t VBYTES = std::is_same<Val, NoValue>::value ? 0 : sizeof(Val);
+  if (!a.planned && !a.src_keys && a.n <= single_tile_items(sizeof(Bits), VBYTES))
+    return caps.rank == Rank::LaneAtomic ? launch_single_tile<Bits, Val, Ops, Rank::LaneAtomic>(a)
+                                         : launch_single_tile<Bits, Val, Ops, Rank::MatchAny>(a);
   uint32_t *bins = reinterpret_cast<uint32_t *>(a.ws + l.bins);
   {
     KernelTimer t("radix_init", a.stream, 0);

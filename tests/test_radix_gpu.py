@@ -264,3 +264,85 @@ def test_double_buffer_selector_parity(launch, dtype, vdtype, n, window, flipped
         np.testing.assert_array_equal(cv.to_host_vec(), want_v)
     np.testing.assert_array_equal(_bits(got), _bits(want))
     assert buffers.current_is_first() == (not flipped)
+
+
+def _single_tile_items(key_bytes, value_bytes):
+    # The reference's single-tile capacity (rccl-cub/src/workspace.rs:22-66).
+    return 256 * max(1, 19 * 4 // max(key_bytes, value_bytes, 4))
+
+
+def _value_array(width, n):
+    if width == 16:
+        return workloads.hash_range(99, 2 * n).view(np.dtype((np.void, 16)))
+    dt = {1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}[width]
+    return (np.arange(n, dtype=np.uint64) % np.uint64(1 << (8 * width - 1))).astype(dt)
+
+
+@pytest.mark.parametrize("kind,width", [("u32", 0), ("i32", 4), ("f32", 8), ("u64", 0),
+                                        ("i64", 4), ("f64", 1), ("u32", 16), ("u64", 2),
+                                        ("f32", 0), ("u64", 8)])
+@pytest.mark.parametrize("descending", [False, True])
+def test_single_tile_route(launch, kind, width, descending):
+    """Inputs up to the single-tile capacity sort in one launch (one block,
+    every pass in LDS), bit-exact with the oracle, ties in input order."""
+    from rccl_amd import _abi
+
+    dt = np.dtype(oracle.KIND_DTYPES[kind])
+    limit = _single_tile_items(dt.itemsize, width)
+    for n in (1, 2, 63, 64, 65, 257, limit - 1, limit):
+        raw = workloads.hash_range(17 * n + width, n)
+        bits = (raw >> np.uint64(64 - 8 * dt.itemsize)).astype(np.dtype(f"u{dt.itemsize}"))
+        bits[::5] = bits[0]  # ties
+        if dt.kind == "f":
+            bits[1::7] = 0
+            bits[2::11] = 1 << (8 * dt.itemsize - 1)
+        host = bits.view(dt)
+        keys = DeviceBuffer.from_host(host)
+        if width:
+            vals_h = _value_array(width, n)
+            vals = DeviceBuffer.from_host(vals_h)
+            ws = cub.device_radix_sort_pairs_workspace(launch, dt, vals_h.dtype, n)
+        else:
+            ws = cub.device_radix_sort_workspace(launch, dt, n)
+        _abi.timing_read()
+        _abi.timing_enable(True)
+        try:
+            if width:
+                (cub.device_radix_sort_pairs_descending if descending
+                 else cub.device_radix_sort_pairs)(launch, keys, vals, ws)
+            else:
+                (cub.device_radix_sort_keys_descending if descending
+                 else cub.device_radix_sort_keys)(launch, keys, ws)
+            launch.synchronize()
+        finally:
+            launches = [name for name, _ms, _items in _abi.timing_read()]
+            _abi.timing_enable(False)
+        assert launches == ["radix_single_tile"], (n, launches)
+        if width:
+            wk, wv = oracle.radix_sort(kind, host, vals_h, descending=descending)
+            assert np.array_equal(vals.to_host_vec().view(np.uint8), wv.view(np.uint8)), n
+        else:
+            wk = oracle.radix_sort(kind, host, descending=descending)
+        assert np.array_equal(_bits(keys.to_host_vec()), _bits(wk)), n
+
+
+@pytest.mark.parametrize("window", [(0, 24), (8, 9), (3, 32), (0, 16)])
+def test_single_tile_windows_flip_once(launch, window):
+    """The DoubleBuffer form of a single-tile sort leaves the result in the
+    other buffer whatever the number of passes (one flip, as the
+    reference's single-tile route)."""
+    n = 4_000
+    host = workloads.uniform_u32(n, 31 + window[0])
+    vals = np.arange(n, dtype=np.uint32)
+    k0, k1 = DeviceBuffer.from_host(host), DeviceBuffer.zeroed(np.uint32, n)
+    v0, v1 = DeviceBuffer.from_host(vals), DeviceBuffer.zeroed(np.uint32, n)
+    buffers = cub.DoubleBuffer.paired((k0, v0), (k1, v1))
+    ws = cub.device_radix_sort_pairs_buffer_workspace(launch, np.uint32, np.uint32, n)
+    cub.device_radix_sort_pairs_buffer(launch, buffers, range(*window), ws)
+    launch.synchronize()
+    assert not buffers.current_is_first()
+    wk, wv = oracle.radix_sort("u32", host, vals, begin_bit=window[0], end_bit=window[1])
+    ck, cv = buffers.current()
+    np.testing.assert_array_equal(ck.to_host_vec(), wk)
+    np.testing.assert_array_equal(cv.to_host_vec(), wv)
+    np.testing.assert_array_equal(k0.to_host_vec(), host)  # the input is left as it was
