@@ -116,8 +116,8 @@ def _steps(*args, **kw):
 def roofline(bytes_per_launch, launch_ms, kernel, traffic=None):
     achieved = bytes_per_launch / (launch_ms * 1e-3) / 1e9
     extra = {} if traffic is None else {
-        "traffic_source": "profiles/hbm_traffic_2p28.txt (rocprofv3 FETCH_SIZE x 2.0 + "
-                          "WRITE_SIZE x 1.0, calibrated on a 1 GiB copy)"}
+        "traffic_source": "profiles/hbm_traffic_bench_legs.txt (rocprofv3 FETCH_SIZE and "
+                          "WRITE_SIZE, each scaled so a 1 GiB copy reads as 1 GiB)"}
     return {
         "bound": "hbm",
         "achieved": round(achieved, 1),
@@ -130,21 +130,23 @@ def roofline(bytes_per_launch, launch_ms, kernel, traffic=None):
     }
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_2p28.txt")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_bench_legs.txt")
 
 
 def profiled_traffic(kernel, log2n):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
     summary (FETCH_SIZE and WRITE_SIZE scaled by a copy kernel of known size),
     or None when that summary does not cover this problem size (the summary
-    is of the default run, whose sizes all derive from --log2n 28)."""
+    is of the default run, whose sizes all derive from --log2n 28). A row is
+    `name kernel... calls read write traffic algorithmic ratio`; the kernel
+    label may hold spaces, so the traffic is read from the right."""
     if log2n != 28 or not os.path.exists(TRAFFIC_PROFILE):
         return None
     with open(TRAFFIC_PROFILE) as f:
         for line in f:
             parts = line.split()
-            if parts and parts[0] == kernel and len(parts) >= 7:
-                return int(parts[6])
+            if len(parts) >= 8 and parts[0] == kernel:
+                return int(parts[-3])
     return None
 
 
@@ -679,27 +681,53 @@ def run_c1_latency(torch, np, cub, abi, DeviceBuffer, wd, steps, warmup):
     }
 
 
+LEGS = ("metric", "pairs", "c1", "c2_uniform", "c2_low_entropy", "c3", "merge", "merge_sort",
+        "set_ops", "record_sort", "compaction", "lower_bound", "cpu_baseline")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=31)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--log2n", type=int, default=28)
+    ap.add_argument("--legs", default=",".join(LEGS),
+                    help="comma-separated legs to run (default: all): " + ", ".join(LEGS))
     ap.add_argument("--no-pairs", action="store_true", help="skip the u64+u32 pairs leg")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the C1, C2 (uniform, low-entropy) and C3 legs")
     ap.add_argument("--no-ordering", action="store_true",
-                    help="skip the C4 merge / merge sort and C5 set operation legs")
+                    help="skip the C4 merge / merge sort, C5 set operation, record sort, "
+                         "compaction and lower_bound legs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ranking", choices=("auto", "lane_atomic", "match_any"), default="auto",
                     help="onesweep ranking mode (rccl_hip_radix_configure)")
     ap.add_argument("--tile-order", choices=("auto", "ticket"), default="auto",
                     help="onesweep tile order (rccl_hip_radix_configure)")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="first copy 1 GiB device to device (a kernel of known traffic for "
+                         "calibrating rocprofv3's FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path).", file=sys.stderr)
         return 2
+    legs = [x for x in args.legs.split(",") if x]
+    unknown = sorted(set(legs) - set(LEGS))
+    if unknown:
+        print(f"unknown legs: {unknown}", file=sys.stderr)
+        return 2
+    skip = set()
+    if args.no_pairs:
+        skip.add("pairs")
+    if args.no_configs:
+        skip.update(("c1", "c2_uniform", "c2_low_entropy", "c3"))
+    if args.no_ordering:
+        skip.update(("merge", "merge_sort", "set_ops", "record_sort", "compaction",
+                     "lower_bound"))
+    if args.no_cpu_baseline:
+        skip.add("cpu_baseline")
+    legs = [x for x in legs if x not in skip]
 
     import numpy as np
     import torch
@@ -715,39 +743,19 @@ def main():
     cub.Program.load(0)
     abi.check(abi.load().rccl_hip_radix_configure(abi.RANKING[args.ranking],
                                                   abi.TILE_ORDER[args.tile_order]))
+    if args.calibration_copy:
+        src = torch.empty(1 << 28, dtype=torch.int32, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     n = 1 << args.log2n
-    _log(f"u32 keys n=2^{args.log2n}")
-    keys_t = wd.metric_u32_keys(n)
-    r32 = run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, None, args.steps, args.warmup)
-    del keys_t
-    _log(f"u32 keys: {r32['ms']:.3f} ms/sort")
-
-    rp = None
-    if not args.no_pairs:
-        pk, pv = wd.metric_pairs(n)
-        rp = run_radix(torch, np, cub, abi, DeviceBuffer, pk, pv, args.steps, args.warmup)
-        del pk, pv
-        _log(f"u64+u32 pairs: {rp['ms']:.3f} ms/sort")
-    torch.cuda.empty_cache()
-
-    gkeys = n / (r32["ms"] * 1e-3) / 1e9
     out = {
-        "metric": METRIC,
-        "value": round(gkeys, 3),
-        "unit": "Gkeys/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(r32["ms"], 4),
-        "ms_per_step_mean": round(r32["ms_mean"], 4),
-        "ms_per_step_min": round(r32["ms_min"], 4),
-        "ms_per_step_wall": round(r32["ms_wall"], 4),
+        "metric": METRIC, "value": None, "unit": "Gkeys/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": None,
         "timing": "ms_per_step is the median of the timed steps' hipEvent intervals (the "
                   "reference's protocol); the input is restored outside each interval",
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "u32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u32",
         "data": f"synthetic: key[i] = splitmix64(0x{workloads.SEEDS['M32']:x} + i) >> 32",
         "config": {
             "workload": "DeviceRadixSort keys-only, u32 ascending, uniform 32-bit keys, "
@@ -755,16 +763,35 @@ def main():
             "n": n,
             "bytes_model": "36 B/key = 4n (histogram read) + 4 x (4n read + 4n write)",
         },
-        "sort_roofline_frac": round(36.0 * n / (r32["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": roofline(8.0 * n, r32["kernel_ms"]["radix_onesweep"],
-                             "radix_onesweep (one 8-bit pass: 4n read + 4n write)",
-                             profiled_traffic("radix_onesweep_u32", args.log2n)),
-        "kernel_ms": _rounded(r32["kernel_ms"]),
         "radix_modes": {"ranking": args.ranking, "tile_order": args.tile_order},
-        "validated": r32["validated"],
+        "legs": legs,
     }
-    valid = r32["validated"]
-    if rp is not None:
+    valid = True
+    if "metric" in legs:
+        _log(f"u32 keys n=2^{args.log2n}")
+        keys_t = wd.metric_u32_keys(n)
+        r32 = run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, None, args.steps, args.warmup)
+        del keys_t
+        _log(f"u32 keys: {r32['ms']:.3f} ms/sort")
+        out.update({
+            "value": round(n / (r32["ms"] * 1e-3) / 1e9, 3),
+            "ms_per_step": round(r32["ms"], 4),
+            "ms_per_step_mean": round(r32["ms_mean"], 4),
+            "ms_per_step_min": round(r32["ms_min"], 4),
+            "ms_per_step_wall": round(r32["ms_wall"], 4),
+            "sort_roofline_frac": round(36.0 * n / (r32["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "roofline": roofline(8.0 * n, r32["kernel_ms"]["radix_onesweep"],
+                                 "radix_onesweep (one 8-bit pass: 4n read + 4n write)",
+                                 profiled_traffic("radix_onesweep_u32", args.log2n)),
+            "kernel_ms": _rounded(r32["kernel_ms"]),
+            "validated": r32["validated"],
+        })
+        valid = valid and r32["validated"]
+    if "pairs" in legs:
+        pk, pv = wd.metric_pairs(n)
+        rp = run_radix(torch, np, cub, abi, DeviceBuffer, pk, pv, args.steps, args.warmup)
+        del pk, pv
+        _log(f"u64+u32 pairs: {rp['ms']:.3f} ms/sort")
         out["pairs"] = radix_leg(
             rp, n, f"DeviceRadixSort pairs, u64 keys uniform over 64 bits, u32 values = index, "
                    f"n=2^{args.log2n}, 8 passes",
@@ -772,27 +799,31 @@ def main():
             "radix_onesweep (one pass: 12n read + 12n write)", "radix_onesweep_pairs",
             args.log2n, "u64 keys + u32 values")
         valid = valid and rp["validated"]
-    if not args.no_configs:
-        log26 = max(args.log2n - 2, 1)
-        n26 = 1 << log26
-        configs = {}
+    torch.cuda.empty_cache()
+    configs = {}
+    log26 = max(args.log2n - 2, 1)
+    n26 = 1 << log26
+    if "c1" in legs:
         _log("C1 latency")
         configs["c1"] = run_c1_latency(torch, np, cub, abi, DeviceBuffer, wd, args.steps,
                                        args.warmup)
-        for name, gen, label in (("c2_uniform", wd.c2_uniform, "uniform over 64 bits"),
-                                 ("c2_low_entropy", wd.c2_low_entropy,
-                                  "256 random values, Zipf s=1.1 frequencies")):
-            _log(name)
-            k, v = gen(n26)
-            r = run_radix(torch, np, cub, abi, DeviceBuffer, k, v, args.steps, args.warmup)
-            del k, v
-            configs[name] = radix_leg(
-                r, n26, f"C2 stable pair sort: 2^{log26} u64 keys ({label}), u32 values = "
-                        "original index, ascending; tie order checked exactly",
-                (200.0, "200 B/pair = 8n + 8 x (12n read + 12n write)"), 24.0,
-                "radix_onesweep (one pass: 12n read + 12n write)", "radix_onesweep_" + name,
-                args.log2n, "u64 keys + u32 values")
-            _log(f"{name}: {r['ms']:.3f} ms")
+    for name, gen, label in (("c2_uniform", wd.c2_uniform, "uniform over 64 bits"),
+                             ("c2_low_entropy", wd.c2_low_entropy,
+                              "256 random values, Zipf s=1.1 frequencies")):
+        if name not in legs:
+            continue
+        _log(name)
+        k, v = gen(n26)
+        r = run_radix(torch, np, cub, abi, DeviceBuffer, k, v, args.steps, args.warmup)
+        del k, v
+        configs[name] = radix_leg(
+            r, n26, f"C2 stable pair sort: 2^{log26} u64 keys ({label}), u32 values = "
+                    "original index, ascending; tie order checked exactly",
+            (200.0, "200 B/pair = 8n + 8 x (12n read + 12n write)"), 24.0,
+            "radix_onesweep (one pass: 12n read + 12n write)", "radix_onesweep_" + name,
+            args.log2n, "u64 keys + u32 values")
+        _log(f"{name}: {r['ms']:.3f} ms")
+    if "c3" in legs:
         _log("c3")
         k = wd.c3_keys(n).view(torch.int32)
         r = run_radix(torch, np, cub, abi, DeviceBuffer, k, None, args.steps, args.warmup,
@@ -806,41 +837,52 @@ def main():
             "radix_onesweep (one 8-bit pass: 4n read + 4n write)", "radix_onesweep_c3",
             args.log2n, "f32 (ordered as u32 bits)")
         _log(f"c3: {r['ms']:.3f} ms")
-        torch.cuda.empty_cache()
+    torch.cuda.empty_cache()
+    if configs:
         out["configs"] = configs
         valid = valid and all(c["validated"] for c in configs.values())
-    if not args.no_ordering:
-        log_each = max(args.log2n - 1, 1)
-        log_sort = max(args.log2n - 2, 1)
+    ordering = {}
+    log_each = max(args.log2n - 1, 1)
+    log_sort = max(args.log2n - 2, 1)
+    if "merge" in legs:
         _log("C4 merge")
-        mg = run_merge(torch, np, cub, abi, DeviceBuffer, wd, log_each, args.steps, args.warmup)
-        _log(f"C4 merge: {mg['ms_per_step']:.3f} ms")
+        ordering["merge"] = run_merge(torch, np, cub, abi, DeviceBuffer, wd, log_each, args.steps,
+                                      args.warmup)
+        _log(f"C4 merge: {ordering['merge']['ms_per_step']:.3f} ms")
+    if "merge_sort" in legs:
         _log("C4 merge sort")
-        ms = run_merge_sort(torch, np, cub, abi, DeviceBuffer, wd, log_sort, args.steps,
-                            args.warmup)
-        _log(f"C4 merge sort: {ms['ms_per_step']:.3f} ms")
+        ordering["merge_sort"] = run_merge_sort(torch, np, cub, abi, DeviceBuffer, wd, log_sort,
+                                                args.steps, args.warmup)
+        _log(f"C4 merge sort: {ordering['merge_sort']['ms_per_step']:.3f} ms")
+    if "set_ops" in legs:
         _log("C5 set operations")
-        so = run_set_ops(torch, np, cub, abi, DeviceBuffer, wd, log_sort, args.steps, args.warmup)
+        ordering["set_ops"] = run_set_ops(torch, np, cub, abi, DeviceBuffer, wd, log_sort,
+                                          args.steps, args.warmup)
         _log("C5 set operations done")
+    if "record_sort" in legs:
         _log("record sort")
-        rsr = run_record_sort(torch, np, abi, DeviceBuffer, wd, workloads, args.steps,
-                              args.warmup)
-        _log(f"record sort: {rsr['ms_per_step']:.3f} ms")
+        ordering["record_sort"] = run_record_sort(torch, np, abi, DeviceBuffer, wd, workloads,
+                                                  args.steps, args.warmup)
+        _log(f"record sort: {ordering['record_sort']['ms_per_step']:.3f} ms")
+    if "compaction" in legs:
         _log("compaction")
-        cp = run_compaction(torch, np, abi, DeviceBuffer, workloads, args.steps, args.warmup)
+        ordering["compaction"] = run_compaction(torch, np, abi, DeviceBuffer, workloads,
+                                                args.steps, args.warmup)
         _log("compaction done")
+    if "lower_bound" in legs:
         _log("search")
-        se = run_search(torch, np, abi, DeviceBuffer, wd, log_sort, max(log_sort - 2, 1),
-                        args.steps, args.warmup)
+        ordering["lower_bound"] = run_search(torch, np, abi, DeviceBuffer, wd, log_sort,
+                                             max(log_sort - 2, 1), args.steps, args.warmup)
         _log("search done")
-        out["ordering"] = {"merge": mg, "merge_sort": ms, "set_ops": so, "record_sort": rsr,
-                           "compaction": cp, "lower_bound": se}
-        valid = valid and rsr["validated"] and cp["unique_copy"]["validated"] and \
-            cp["reduce_by_key"]["validated"] and se["validated"]
-        valid = valid and mg["validated"] and ms["validated"] and all(
-            so[op]["validated"] for op in ("union", "intersection", "difference",
-                                           "symmetric_difference"))
-    if not args.no_cpu_baseline:
+    if ordering:
+        out["ordering"] = ordering
+        for leg in ordering.values():
+            if "validated" in leg:
+                valid = valid and bool(leg["validated"])
+            else:
+                valid = valid and all(v["validated"] for v in leg.values()
+                                      if isinstance(v, dict) and "validated" in v)
+    if "cpu_baseline" in legs:
         _log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline()
     out["validated"] = bool(valid)

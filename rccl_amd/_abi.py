@@ -13,7 +13,9 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "librccl_hip.so")
+# The in-tree build; RCCL_HIP_LIBRARY may name another build of the same
+# library (for example one compiled with different tuning macros).
+LIB_PATH = os.environ.get("RCCL_HIP_LIBRARY") or os.path.join(HERE, "librccl_hip.so")
 
 # Enumerations (values equal include/rccl_hip.h).
 SUCCESS = 0
