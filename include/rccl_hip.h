@@ -199,9 +199,11 @@ enum {
   RCCL_HIP_TILE_ORDER_TICKET = 1 /* every block claims its tile from an atomic ticket */
 };
 
-/* Selects how the radix sort ranks keys within a tile and how blocks find
- * their tiles, for every later call in the process (every radix path: radix
- * sort, the merge-sort lowering and the record sort). No counterpart in the
+/* Selects how the radix sort ranks keys within a tile (every radix path:
+ * radix sort, the merge-sort lowering and the record sort) and how blocks find
+ * their tiles (those paths, and the set operations and compactions, whose
+ * look-backs order tiles the same way), for every later call in the process.
+ * No counterpart in the
  * reference, whose onesweep always ranks with match-any and claims tiles
  * from a ticket (rccl-cub/src/ordering_backend/radix.rs:918-938, :1078-1087).
  * The output is identical in every mode; the defaults are the fastest ones

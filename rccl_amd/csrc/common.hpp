@@ -56,6 +56,12 @@ rccl_hip_status resident_blocks(const void *kernel, int threads, size_t *blocks)
 // that a device too small for it reports an error instead of waiting forever.
 rccl_hip_status check_xcd_rows(const void *kernel, int threads, uint32_t run, const char *role);
 
+// Tile order for the current device: XCDS where its blocks land on the XCDs
+// round-robin (XCD-ordered tiles), 1 where tiles must be claimed from an
+// atomic ticket (the load-time probe failed, or rccl_hip_radix_configure
+// asked for tickets).
+rccl_hip_status tile_order(uint32_t *nx);
+
 inline size_t key_bytes(rccl_hip_key_kind k) {
   switch (k) {
   case RCCL_HIP_KEY_U32: case RCCL_HIP_KEY_I32: case RCCL_HIP_KEY_F32: return 4;
@@ -86,6 +92,14 @@ __device__ __forceinline__ uint32_t lane_id() {
 __device__ __forceinline__ uint32_t popc_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+// Workgroup barrier that orders LDS only: global loads and stores issued
+// before it stay in flight (__syncthreads would wait for all of them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Device-scope (agent) atomics: visible across all XCDs of the GPU.

@@ -10,7 +10,8 @@
 // a run's aggregate is a left fold, ((v0 op v1) op v2) ..., in index order.
 // The reference marks run heads, scans them and folds each run on one thread
 // in three launches. Here one pass over the input does all of it:
-//   tile    one block per tile (tiles in XCD order, xcd_order_tile): keys
+//   tile    one block per tile (tiles in XCD order or from a ticket,
+//           lookback::claim_tile): keys
 //           (and values) staged in LDS, run heads per thread, a block scan
 //           of the head counts, the tile's output offset from a two-level
 //           decoupled look-back (tile_lookback.hpp); for a reduction the
@@ -134,7 +135,8 @@ group_tile_kernel(const K *__restrict__ keys, const P *__restrict__ pays,
                   const typename Op::Value *__restrict__ vals, size_t n, size_t tiles,
                   K *__restrict__ out_keys, P *__restrict__ out_pays,
                   typename Op::Value *__restrict__ out_vals, uint64_t *__restrict__ out_count,
-                  uint64_t *desc, uint64_t *gagg, uint64_t *ginc) {
+                  uint64_t *desc, uint64_t *gagg, uint64_t *ginc, uint64_t *ticket,
+                  uint32_t nx) {
   using V = typename Op::Value;
   using Smem = TileSmem<K, P, V, ITEMS>;
   constexpr bool HAS_P = Smem::HAS_P;
@@ -145,8 +147,10 @@ group_tile_kernel(const K *__restrict__ keys, const P *__restrict__ pays,
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
-  // XCD order: every tile a look-back waits on has been started.
-  const size_t t = xcd_order_tile<XCD_RUN>(blockIdx.x);
+  // XCD order or a ticket (claim_tile): every tile a look-back waits on has
+  // been started.
+  __shared__ uint64_t s_tile;
+  const size_t t = lookback::claim_tile<XCD_RUN>(nx, ticket, s_tile);
   if (t >= tiles) return;
   const size_t base = t * TILE;
   const uint32_t len = static_cast<uint32_t>(std::min<size_t>(TILE, n - base));
@@ -293,7 +297,7 @@ struct GroupArgs {
 
 struct Layout {
   size_t tiles = 0, groups = 0;
-  size_t desc = 0, gagg = 0, ginc = 0, total = 0;
+  size_t desc = 0, gagg = 0, ginc = 0, ticket = 0, total = 0;
 };
 
 template <class K, class P, class V>
@@ -304,12 +308,14 @@ Layout layout(size_t n) {
   l.tiles = (n + TILE - 1) / TILE;
   l.groups = (l.tiles + lookback::GROUP - 1) / lookback::GROUP;
   size_t off = 0;
-  l.desc = off;  // descriptors and group words are contiguous
+  l.desc = off;  // descriptors, group words and the ticket are contiguous
   off += l.tiles * sizeof(uint64_t);
   l.gagg = off;
   off += l.groups * sizeof(uint64_t);
   l.ginc = off;
   off += l.groups * sizeof(uint64_t);
+  l.ticket = off;
+  off += sizeof(uint64_t);
   l.total = align_up(off, 256);
   return l;
 }
@@ -328,8 +334,12 @@ rccl_hip_status run(const GroupArgs &a) {
   unsigned char *ws = static_cast<unsigned char *>(a.ws);
   uint64_t *desc = reinterpret_cast<uint64_t *>(ws + l.desc);
   const size_t words = lookback::state_words(l.tiles);
-  RCCL_HIP_TRY(check_xcd_rows(reinterpret_cast<const void *>(&group_tile_kernel<K, P, Op, ITEMS>),
-                              THREADS, XCD_RUN, "group tile does not fit on the device"));
+  uint32_t nx = 1;
+  RCCL_HIP_TRY(tile_order(&nx));
+  if (nx == XCDS)
+    RCCL_HIP_TRY(check_xcd_rows(
+        reinterpret_cast<const void *>(&group_tile_kernel<K, P, Op, ITEMS>), THREADS, XCD_RUN,
+        "group tile does not fit on the device"));
   {
     KernelTimer t("group_clear", a.stream, words);
     group_clear_kernel<<<dim3(static_cast<uint32_t>(std::min<size_t>((words + 255) / 256, 1024))),
@@ -339,11 +349,13 @@ rccl_hip_status run(const GroupArgs &a) {
   {
     KernelTimer t("group_tile", a.stream, a.n);
     group_tile_kernel<K, P, Op, ITEMS>
-        <<<dim3(static_cast<uint32_t>(xcd_order_grid(l.tiles, XCD_RUN))), THREADS, 0, a.stream>>>(
+        <<<dim3(static_cast<uint32_t>(nx == XCDS ? xcd_order_grid(l.tiles, XCD_RUN) : l.tiles)),
+           THREADS, 0, a.stream>>>(
         static_cast<const K *>(a.keys), static_cast<const P *>(a.pays),
         static_cast<const V *>(a.vals), a.n, l.tiles, static_cast<K *>(a.out_keys),
         static_cast<P *>(a.out_pays), static_cast<V *>(a.out_vals), a.out_count, desc,
-        reinterpret_cast<uint64_t *>(ws + l.gagg), reinterpret_cast<uint64_t *>(ws + l.ginc));
+        reinterpret_cast<uint64_t *>(ws + l.gagg), reinterpret_cast<uint64_t *>(ws + l.ginc),
+        reinterpret_cast<uint64_t *>(ws + l.ticket), nx);
   }
   return check_launch("group tile");
 }

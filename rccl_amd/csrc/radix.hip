@@ -194,6 +194,17 @@ rccl_hip_status device_caps(DeviceCaps *caps) {
   return ok();
 }
 
+} // namespace radix
+
+rccl_hip_status tile_order(uint32_t *nx) {
+  radix::DeviceCaps c;
+  RCCL_HIP_TRY(radix::device_caps(&c));
+  *nx = c.nx;
+  return ok();
+}
+
+namespace radix {
+
 namespace {
 
 bool radix_kind(rccl_hip_key_kind k) { return k >= RCCL_HIP_KEY_U32 && k <= RCCL_HIP_KEY_F64; }

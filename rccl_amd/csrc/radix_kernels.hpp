@@ -404,14 +404,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Workgroup barrier that orders LDS only: global loads and stores issued
-// before it stay in flight (__syncthreads would wait for all of them).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Tile processed by a block, in XCD order (xcd_order_tile): the cache lines
 // that neighbouring tiles both write at digit-run boundaries are merged in
 // their shared L2 instead of reaching HBM as two partial writes. This is used

@@ -266,7 +266,7 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
             const V *__restrict__ bv, const uint64_t *__restrict__ splits, size_t tiles,
             K *__restrict__ out, V *__restrict__ outv, size_t out_cap,
             uint64_t *__restrict__ out_count, uint64_t *desc, uint64_t *gagg, uint64_t *ginc,
-            Arith<K> ar, Arith<K> br) {
+            uint64_t *ticket, uint32_t nx, Arith<K> ar, Arith<K> br) {
   using Smem = TileSmem<K, V, ITEMS>;
   constexpr bool PAIRS = Smem::PAIRS;
   constexpr bool VALS_B = PAIRS && (OP == UNION || OP == SYMMETRIC_DIFFERENCE);
@@ -275,10 +275,11 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
-  // Tiles in XCD order: every tile a look-back waits on has been started
-  // (xcd_order_tile), with no atomic ticket to take first, and neighbouring
-  // tiles share an L2.
-  const size_t t = xcd_order_tile<XCD_RUN>(blockIdx.x);
+  // Tiles in XCD order (no atomic to take first; neighbouring tiles share an
+  // L2) or, where the device's placement is not round-robin, from a ticket:
+  // either way every tile a look-back waits on has been started.
+  __shared__ uint64_t s_tile;
+  const size_t t = lookback::claim_tile<XCD_RUN>(nx, ticket, s_tile);
   if (t >= tiles) return;
   const size_t i0 = splits[2 * t], j0 = splits[2 * t + 1];
   const size_t i1 = splits[2 * t + 2], j1 = splits[2 * t + 3];
@@ -443,7 +444,7 @@ struct SetArgs {
 
 struct Layout {
   size_t tiles = 0, groups = 0;
-  size_t splits = 0, desc = 0, gagg = 0, ginc = 0, total = 0;
+  size_t splits = 0, desc = 0, gagg = 0, ginc = 0, ticket = 0, total = 0;
 };
 
 template <class K, class V>
@@ -462,6 +463,8 @@ Layout layout(size_t na, size_t nb) {
   off += l.groups * sizeof(uint64_t);
   l.ginc = off;
   off += l.groups * sizeof(uint64_t);
+  l.ticket = off;
+  off += sizeof(uint64_t);
   l.total = align_up(off, 256);
   return l;
 }
@@ -479,12 +482,16 @@ rccl_hip_status run_op(const SetArgs &s) {
   uint64_t *desc = reinterpret_cast<uint64_t *>(ws + l.desc);
   uint64_t *gagg = reinterpret_cast<uint64_t *>(ws + l.gagg);
   uint64_t *ginc = reinterpret_cast<uint64_t *>(ws + l.ginc);
-  // Descriptors and group words are contiguous.
-  const size_t state_words = l.tiles + 2 * l.groups;
-  RCCL_HIP_TRY(check_xcd_rows(
-      s.arith ? reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, true>)
-              : reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, false>),
-      THREADS, XCD_RUN, "set tile does not fit on the device"));
+  uint64_t *ticket = reinterpret_cast<uint64_t *>(ws + l.ticket);
+  // Descriptors, group words and the ticket are contiguous.
+  const size_t state_words = lookback::state_words(l.tiles);
+  uint32_t nx = 1;
+  RCCL_HIP_TRY(tile_order(&nx));
+  if (nx == XCDS)
+    RCCL_HIP_TRY(check_xcd_rows(
+        s.arith ? reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, true>)
+                : reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, false>),
+        THREADS, XCD_RUN, "set tile does not fit on the device"));
   {
     KernelTimer t("set_clear", s.stream, state_words);
     clear_kernel<<<dim3(static_cast<uint32_t>(std::min<size_t>((state_words + 255) / 256, 1024))),
@@ -492,7 +499,7 @@ rccl_hip_status run_op(const SetArgs &s) {
   }
   RCCL_HIP_TRY(check_launch("set clear"));
   const dim3 pgrid(static_cast<uint32_t>((l.tiles + 1 + 255) / 256));
-  const dim3 tgrid(static_cast<uint32_t>(xcd_order_grid(l.tiles, XCD_RUN)));
+  const dim3 tgrid(static_cast<uint32_t>(nx == XCDS ? xcd_order_grid(l.tiles, XCD_RUN) : l.tiles));
   const K *a = static_cast<const K *>(s.a);
   const K *b = static_cast<const K *>(s.b);
   const V *av = static_cast<const V *>(s.av);
@@ -516,7 +523,7 @@ rccl_hip_status run_op(const SetArgs &s) {
         KernelTimer t("set_tile", s.stream, s.na + s.nb);
         tile_kernel<K, V, Cmp, OP, ITEMS, true><<<tgrid, THREADS, 0, s.stream>>>(
             a, av, b, bv, splits, l.tiles, out, outv, s.out_cap, s.out_count, desc, gagg, ginc,
-            ar, br);
+            ticket, nx, ar, br);
       }
       return check_launch("set tile");
     } else {
@@ -534,7 +541,7 @@ rccl_hip_status run_op(const SetArgs &s) {
     KernelTimer t("set_tile", s.stream, s.na + s.nb);
     tile_kernel<K, V, Cmp, OP, ITEMS, false><<<tgrid, THREADS, 0, s.stream>>>(
         a, av, b, bv, splits, l.tiles, out, outv, s.out_cap, s.out_count, desc, gagg, ginc,
-        Arith<K>{}, Arith<K>{});
+        ticket, nx, Arith<K>{}, Arith<K>{});
   }
   return check_launch("set tile");
 }

@@ -1,7 +1,7 @@
 // Two-level decoupled look-back over per-tile counts, for kernels whose tiles
 // are numbered so that every tile a look-back waits on has been started
-// (xcd_order_tile) and that need each tile's exclusive prefix: the set
-// operations' and the compactions' output offsets.
+// (claim_tile: XCD order or an atomic ticket) and that need each tile's
+// exclusive prefix: the set operations' and the compactions' output offsets.
 //
 // Every tile publishes its count at once (flag AGG) and, after its look-back,
 // its inclusive prefix (flag INCL); it also adds (1 << GA_SHIFT) | count to
@@ -99,11 +99,27 @@ __device__ __forceinline__ uint64_t tile_prefix(size_t t, size_t tiles, uint64_t
   return prefix;
 }
 
-// Words of look-back state for `tiles` tiles: descriptors, group aggregates
-// and group prefixes; all zeroed before a launch.
+// Words of look-back state for `tiles` tiles: descriptors, group aggregates,
+// group prefixes and the tile ticket (in that order, contiguous); all zeroed
+// before a launch.
 inline size_t state_words(size_t tiles) {
   const size_t groups = (tiles + GROUP - 1) / GROUP;
-  return tiles + 2 * groups;
+  return tiles + 2 * groups + 1;
+}
+
+// Tile of the calling block. Where the device places the blocks of a launch
+// on its XCDs round-robin (nx == XCDS, probed when the program is loaded),
+// tiles go in XCD order (xcd_order_tile): neighbouring tiles share an L2 and
+// no atomic is taken. Otherwise the block claims its tile from an atomic
+// ticket: a tile is only claimed by a started block, so the lowest unfinished
+// tile never waits on an unstarted one, whatever the placement. `slot` is a
+// __shared__ word; every thread of the block calls this.
+template <uint32_t RUN>
+__device__ __forceinline__ size_t claim_tile(uint32_t nx, uint64_t *ticket, uint64_t &slot) {
+  if (nx == XCDS) return xcd_order_tile<RUN>(blockIdx.x);
+  if (threadIdx.x == 0) slot = add_agent(ticket, uint64_t(1));
+  __syncthreads();
+  return static_cast<size_t>(slot);
 }
 
 } // namespace lookback

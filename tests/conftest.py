@@ -53,3 +53,16 @@ def radix_ranking(request, launch):
     _abi.check(lib.rccl_hip_radix_configure(_abi.RANKING[ranking], _abi.TILE_ORDER[order]))
     yield request.param
     _abi.check(lib.rccl_hip_radix_configure(0, 0))
+
+
+@pytest.fixture(params=["auto", "ticket"])
+def tile_order(request, launch):
+    """Runs a look-back test (set operations, compactions) with the device's
+    default tile order (XCD order on gfx950) and with every block claiming
+    its tile from an atomic ticket. The output must be identical."""
+    from rccl_amd import _abi
+
+    lib = _abi.load()
+    _abi.check(lib.rccl_hip_radix_configure(0, _abi.TILE_ORDER[request.param]))
+    yield request.param
+    _abi.check(lib.rccl_hip_radix_configure(0, 0))

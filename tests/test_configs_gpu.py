@@ -213,3 +213,4 @@ def test_c3_full_size_device_checks(launch):
     # Infinities at the ends of the numbers, denormals around the zeros.
     assert bool(torch.isposinf(rest[:counts["+inf"]]).all())
     assert bool(torch.isneginf(rest[rest.numel() - counts["-inf"]:]).all())
+

@@ -16,7 +16,7 @@ from rccl_amd import record_sort as rs
 from rccl_amd import thrust, workloads
 from rccl_amd.device import DeviceBuffer
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("tile_order")]
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.json")
 NP = {"u8": np.uint8, "i8": np.int8, "u16": np.uint16, "i16": np.int16, "u32": np.uint32,

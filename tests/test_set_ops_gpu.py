@@ -13,7 +13,7 @@ import oracle
 from rccl_amd import cub, thrust, workloads
 from rccl_amd.device import DeviceBuffer
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("tile_order")]
 
 OPS = ["union", "intersection", "difference", "symmetric_difference"]
 DTYPES = {"u8": np.uint8, "i8": np.int8, "u16": np.uint16, "i16": np.int16, "u32": np.uint32,
