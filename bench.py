@@ -370,6 +370,8 @@ def run_merge(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup):
         "value": round(total / (ms * 1e-3) / 1e9, 3), "unit": "Gkeys/s (outputs)",
         "ms_per_step": round(ms, 4), "ms_per_step_wall": round(wall, 4),
         "bytes_model": "16 B/output = 8 B read (key + value) + 8 B written",
+        # The whole call (partition + merge) against the same bytes.
+        "leg_roofline_frac": round(16.0 * total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": roofline(16.0 * total, kms["merge"], "merge (one launch merges everything)",
                              profiled_traffic("merge", log2_each + 1)),
         "kernel_ms": _rounded(kms), "validated": bool(ok),
@@ -467,6 +469,9 @@ def run_set_ops(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup)
         results[op] = {
             "ms_per_step": round(ms, 4), "output": m,
             "value": round(2 * n_each / (ms * 1e-3) / 1e9, 3), "unit": "Gkeys/s (inputs)",
+            # The whole call (clear + partition + tile) against the tile's bytes.
+            "leg_roofline_frac": round((16.0 * n_each + 8.0 * m) / (ms * 1e-3) / 1e9 /
+                                       HBM_PEAK_GBS, 4),
             "roofline": roofline(16.0 * n_each + 8.0 * m, kms["set_tile"],
                                  "set_tile (reads both inputs, writes the result)",
                                  profiled_traffic("set_tile_" + op, log2_each + 2)),
