@@ -201,6 +201,41 @@ def test_merge_pairs_vs_oracle(launch, kind, width):
             assert gv.tobytes() == wv.tobytes(), (kind, width, na, nb, descending)
 
 
+def _sampled_shapes(kind):
+    """Merges of at least 512 tiles (the sampled partition: every 2,048th A
+    item bracketed against the sampled B items), with the shapes that stress
+    its bounds: heavy duplicates, one side far shorter, all keys equal,
+    disjoint ranges either way round, lengths that are not multiples of the
+    sample stride."""
+    n = 1 << 21
+    dt = np.dtype(DTYPES[kind])
+    rnd = lambda size, seed, distinct=None: _random_keys(kind, size, seed, distinct)
+    lo, hi = (np.iinfo(dt).min, np.iinfo(dt).max)
+    yield "dups", rnd(n + 3, 11, 37), rnd(n - 5, 12, 37)
+    yield "uniform", rnd(n, 13), rnd(n + 2047, 14)
+    yield "short_b", rnd(3 * n + 1, 15, 1000), rnd(5000, 16, 1000)
+    yield "short_a", rnd(777, 17), rnd(2 * n + 17, 18)
+    yield "all_equal", np.full(n + 1, 7, dt), np.full(n - 1, 7, dt)
+    yield "a_before_b", np.full(n, lo, dt), np.full(n + 9, hi, dt)
+    yield "b_before_a", np.full(n + 9, hi, dt), np.full(n, lo, dt)
+
+
+@pytest.mark.parametrize("kind", ["u8", "i16", "u32", "i32", "u64", "i64"])
+@pytest.mark.parametrize("descending", [False, True])
+def test_merge_sampled_partition_vs_oracle(launch, kind, descending):
+    for idx, (name, a, b) in enumerate(_sampled_shapes(kind)):
+        a, b = _sorted(kind, a, descending), _sorted(kind, b, descending)
+        if idx % 2:
+            av, bv = _values(4, a.size, 40 + idx), _values(4, b.size, 50 + idx)
+            gk, gv = _merge(launch, kind, a, b, av, bv, descending)
+            wk, wv = oracle.merge(kind, a, b, av, bv, descending)
+            assert np.array_equal(gv, wv), (kind, name, descending)
+        else:
+            gk = _merge(launch, kind, a, b, descending=descending)
+            wk = oracle.merge(kind, a, b, descending=descending)
+        assert np.array_equal(_bits(gk), _bits(wk)), (kind, name, descending)
+
+
 SORT_SIZES = [0, 1, 2, 255, 256, 4095, 4096, 4097, 12_289, 100_000]
 
 
