@@ -52,6 +52,15 @@ template <class K, class V>
 constexpr size_t tile_items() {
   return size_t(THREADS) * items_for<K, V>();
 }
+// Partition tiles per block (and per look-back tile): two for keys only,
+// whose two register sets of outputs fit; one where values double them.
+#ifndef RCCL_SET_SUB_TILES
+#define RCCL_SET_SUB_TILES 2
+#endif
+template <class K, class V>
+constexpr int sub_tiles_for() {
+  return std::is_same<V, NoValue>::value ? RCCL_SET_SUB_TILES : 1;
+}
 
 // Finite arithmetic input range: item i is start + step * i in the key's own
 // wrapping integer arithmetic (rccl-cub/src/ordering_backend/set.rs:49-81,
@@ -260,16 +269,34 @@ __device__ __forceinline__ void serial_step(const K &ka, const K &kb, bool a_ok,
   adv_b = live && !a_sel;
 }
 
-template <class K, class V, class Cmp, int OP, int ITEMS, bool ARITH>
-__global__ void __launch_bounds__(THREADS)
+// Outputs of one partition tile, held in registers until the block's output
+// offset is known.
+template <class K, class VS, int ITEMS, bool PAIRS>
+struct SubTile {
+  K outk[ITEMS];
+  VS outv[PAIRS ? ITEMS : 1];
+  uint32_t mask;   // emitted items of this thread
+  uint32_t excl;   // this thread's first output within the sub-tile
+  uint32_t count;  // the sub-tile's outputs
+};
+
+// One block handles SUB consecutive partition tiles (a look-back tile): each
+// is staged, partitioned and run through the serial operation in turn, its
+// outputs kept in registers; the block then publishes one count and looks
+// back once for all of them, and stores them in turn. SUB = 2 halves the
+// look-backs at the same LDS footprint (two blocks per CU).
+// Two blocks per CU (4 waves per SIMD): a register budget of 128.
+template <class K, class V, class Cmp, int OP, int ITEMS, int SUB, bool ARITH>
+__global__ void __launch_bounds__(THREADS, 4)
 tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restrict__ b,
             const V *__restrict__ bv, const uint64_t *__restrict__ splits, size_t tiles,
-            K *__restrict__ out, V *__restrict__ outv, size_t out_cap,
+            size_t lb_tiles, K *__restrict__ out, V *__restrict__ outv, size_t out_cap,
             uint64_t *__restrict__ out_count, uint64_t *desc, uint64_t *gagg, uint64_t *ginc,
             uint64_t *ticket, uint32_t nx, Arith<K> ar, Arith<K> br) {
   using Smem = TileSmem<K, V, ITEMS>;
   constexpr bool PAIRS = Smem::PAIRS;
   constexpr bool VALS_B = PAIRS && (OP == UNION || OP == SYMMETRIC_DIFFERENCE);
+  using VS = typename std::conditional<PAIRS, V, char>::type;
   __shared__ Smem sm;
   const Cmp less{};
   const uint32_t tid = threadIdx.x;
@@ -280,20 +307,18 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
   // either way every tile a look-back waits on has been started.
   __shared__ uint64_t s_tile;
   const size_t t = lookback::claim_tile<XCD_RUN>(nx, ticket, s_tile);
-  if (t >= tiles) return;
-  const size_t i0 = splits[2 * t], j0 = splits[2 * t + 1];
-  const size_t i1 = splits[2 * t + 2], j1 = splits[2 * t + 3];
-  const uint32_t la = static_cast<uint32_t>(i1 - i0);
-  const uint32_t lb = static_cast<uint32_t>(j1 - j0);
-  const uint32_t len = la + lb;
+  if (t >= lb_tiles) return;
 
-  // Stage A then B (striped, coalesced). A fixed, unrolled number of loads
-  // per thread, all issued before the first LDS write; each item loads from
-  // A or B through a per-lane address, clamped to the tile's last item.
-  {
-    constexpr int STAGE = (Smem::CAP + THREADS - 1) / THREADS;
-    K kr[STAGE];
-    typename std::conditional<PAIRS, V, char>::type vr[PAIRS ? STAGE : 1];
+  // A partition tile's inputs, loaded into registers: a fixed, unrolled
+  // number of loads per thread, each from A or B through a per-lane address,
+  // clamped to the tile's last item (striped, so the loads coalesce).
+  constexpr int STAGE = (Smem::CAP + THREADS - 1) / THREADS;
+  K kr[STAGE];
+  VS vr[PAIRS ? STAGE : 1];
+  auto load_tile = [&](size_t pt) {
+    const size_t i0 = splits[2 * pt], j0 = splits[2 * pt + 1];
+    const uint32_t la = static_cast<uint32_t>(splits[2 * pt + 2] - i0);
+    const uint32_t len = la + static_cast<uint32_t>(splits[2 * pt + 3] - j0);
 #pragma unroll
     for (int k = 0; k < STAGE; ++k) {
       const uint32_t i = min(uint32_t(k) * THREADS + tid, len ? len - 1u : 0u);
@@ -307,6 +332,30 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
         else vr[k] = from_a ? av[i0 + i] : V{};
       }
     }
+  };
+  if (t * SUB < tiles) load_tile(t * SUB);
+
+  // Barriers order LDS only (lds_barrier): the next sub-tile's loads, issued
+  // right after the current one is staged, stay in flight through its merge.
+  SubTile<K, VS, ITEMS, PAIRS> sub[SUB];
+#pragma unroll
+  for (int s = 0; s < SUB; ++s) {
+    SubTile<K, VS, ITEMS, PAIRS> &r = sub[s];
+    const size_t pt = t * SUB + s;
+    if (pt >= tiles) {  // uniform: the last look-back tile may be short
+      r.mask = 0;
+      r.excl = 0;
+      r.count = 0;
+      continue;
+    }
+    const size_t i0 = splits[2 * pt], j0 = splits[2 * pt + 1];
+    const size_t i1 = splits[2 * pt + 2], j1 = splits[2 * pt + 3];
+    const uint32_t la = static_cast<uint32_t>(i1 - i0);
+    const uint32_t lb = static_cast<uint32_t>(j1 - j0);
+    const uint32_t len = la + lb;
+
+    // Stage the registers into LDS (the previous sub-tile's readers are past
+    // its scan barrier), then load the next sub-tile.
 #pragma unroll
     for (int k = 0; k < STAGE; ++k) {
       const uint32_t i = uint32_t(k) * THREADS + tid;
@@ -315,111 +364,120 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
         if constexpr (PAIRS) sm.vals[i] = vr[k];
       }
     }
-  }
-  __syncthreads();
+    lds_barrier();
+    if (s + 1 < SUB && pt + 1 < tiles) load_tile(pt + 1);
 
-  // Per-thread balanced-path splits (diagonal tid * ITEMS of this tile).
-  {
-    const K *ka = sm.keys;
-    const K *kb = sm.keys + la;
-    size_t si, sj;
-    const uint32_t diag = min(tid * uint32_t(ITEMS), len);
-    balanced_path<false, K>([&](size_t x) { return ka[x]; }, la,
-                                          [&](size_t x) { return kb[x]; }, lb, diag, less, si,
-                                          sj);
-    // Every split lies inside the tile; the star of a diagonal past the end
-    // is clamped.
-    sm.split_a[tid] = static_cast<uint32_t>(min<size_t>(si, la));
-    sm.split_b[tid] = static_cast<uint32_t>(min<size_t>(sj, lb));
-    if (tid == 0) {
-      sm.split_a[THREADS] = la;
-      sm.split_b[THREADS] = lb;
+    // Per-thread balanced-path splits (diagonal tid * ITEMS of this tile).
+    {
+      const K *ka = sm.keys;
+      const K *kb = sm.keys + la;
+      size_t si, sj;
+      const uint32_t diag = min(tid * uint32_t(ITEMS), len);
+      balanced_path<false, K>([&](size_t x) { return ka[x]; }, la,
+                              [&](size_t x) { return kb[x]; }, lb, diag, less, si, sj);
+      // Every split lies inside the tile; the star of a diagonal past the end
+      // is clamped.
+      sm.split_a[tid] = static_cast<uint32_t>(min<size_t>(si, la));
+      sm.split_b[tid] = static_cast<uint32_t>(min<size_t>(sj, lb));
+      if (tid == 0) {
+        sm.split_a[THREADS] = la;
+        sm.split_b[THREADS] = lb;
+      }
     }
-  }
-  __syncthreads();
+    lds_barrier();
 
-  // Serial operation over this thread's A and B ranges.
-  uint32_t ia = sm.split_a[tid], ib = sm.split_b[tid];
-  const uint32_t ea = max(ia, sm.split_a[tid + 1]), eb = max(ib, sm.split_b[tid + 1]);
-  K outk[ITEMS];
-  uint32_t src[PAIRS ? ITEMS : 1];
-  uint32_t mask = 0;
-  // The heads live in registers; a step reloads only the side it advanced.
-  const uint32_t last = len ? len - 1u : 0u;
-  K ka = sm.keys[min(ia, last)];
-  K kb = sm.keys[min(la + ib, last)];
+    // Serial operation over this thread's A and B ranges.
+    uint32_t ia = sm.split_a[tid], ib = sm.split_b[tid];
+    const uint32_t ea = max(ia, sm.split_a[tid + 1]), eb = max(ib, sm.split_b[tid + 1]);
+    uint32_t src[PAIRS ? ITEMS : 1];
+    uint32_t mask = 0;
+    // The heads live in registers; a step reloads only the side it advanced.
+    const uint32_t last = len ? len - 1u : 0u;
+    K ka = sm.keys[min(ia, last)];
+    K kb = sm.keys[min(la + ib, last)];
 #pragma unroll
-  for (int k = 0; k < ITEMS; ++k) {
-    const bool a_ok = ia < ea, b_ok = ib < eb;
-    bool emit, emit_b, adv_a, adv_b;
-    serial_step<OP, K>(ka, kb, a_ok, b_ok, less, emit, emit_b, adv_a, adv_b);
-    outk[k] = emit_b ? kb : ka;
-    if constexpr (PAIRS) src[k] = emit_b ? la + ib : ia;
-    mask |= emit ? (1u << k) : 0u;
-    ia += adv_a ? 1u : 0u;
-    ib += adv_b ? 1u : 0u;
-    if (k + 1 < ITEMS) {
-      if (adv_a) ka = sm.keys[min(ia, last)];
-      if (adv_b) kb = sm.keys[min(la + ib, last)];
+    for (int k = 0; k < ITEMS; ++k) {
+      const bool a_ok = ia < ea, b_ok = ib < eb;
+      bool emit, emit_b, adv_a, adv_b;
+      serial_step<OP, K>(ka, kb, a_ok, b_ok, less, emit, emit_b, adv_a, adv_b);
+      r.outk[k] = emit_b ? kb : ka;
+      if constexpr (PAIRS) src[k] = emit_b ? la + ib : ia;
+      mask |= emit ? (1u << k) : 0u;
+      ia += adv_a ? 1u : 0u;
+      ib += adv_b ? 1u : 0u;
+      if (k + 1 < ITEMS) {
+        if (adv_a) ka = sm.keys[min(ia, last)];
+        if (adv_b) kb = sm.keys[min(la + ib, last)];
+      }
     }
-  }
-  const uint32_t mine = __popc(mask);
-  V outv_reg[PAIRS ? ITEMS : 1];
-  if constexpr (PAIRS) {
+    const uint32_t mine = __popc(mask);
+    r.mask = mask;
+    if constexpr (PAIRS) {
 #pragma unroll
-    for (int k = 0; k < ITEMS; ++k) outv_reg[k] = sm.vals[min(src[k], len ? len - 1 : 0u)];
-  }
+      for (int k = 0; k < ITEMS; ++k) r.outv[k] = sm.vals[min(src[k], last)];
+    }
 
-  // Block-wide exclusive scan of the emitted counts.
-  const uint32_t inc = wave_inclusive_sum(mine, lane);
-  if (lane == 63) sm.wave_total[wave] = inc;
-  __syncthreads();
-  uint32_t excl = inc - mine;
-  uint32_t tile_count = 0;
+    // Block-wide exclusive scan of the emitted counts.
+    const uint32_t inc = wave_inclusive_sum(mine, lane);
+    if (lane == 63) sm.wave_total[wave] = inc;
+    lds_barrier();
+    r.excl = inc - mine;
+    r.count = 0;
 #pragma unroll
-  for (int w = 0; w < WAVES; ++w) {
-    if (uint32_t(w) < wave) excl += sm.wave_total[w];
-    tile_count += sm.wave_total[w];
+    for (int w = 0; w < WAVES; ++w) {
+      if (uint32_t(w) < wave) r.excl += sm.wave_total[w];
+      r.count += sm.wave_total[w];
+    }
+    // The next sub-tile's scan writes wave_total only after two more
+    // barriers, which every reader above has passed.
   }
+  uint32_t total = 0;
+#pragma unroll
+  for (int s = 0; s < SUB; ++s) total += sub[s].count;
 
-  // Two-level decoupled look-back for the tile's output offset (wave 0).
+  // Two-level decoupled look-back for the block's output offset (wave 0).
   if (wave == 0) {
-    const uint64_t prefix =
-        lookback::tile_prefix(t, tiles, tile_count, desc, gagg, ginc, lane);
+    const uint64_t prefix = lookback::tile_prefix(t, lb_tiles, total, desc, gagg, ginc, lane);
     if (lane == 0) {
-      if (t + 1 == tiles && out_count) *out_count = prefix + tile_count;
+      if (t + 1 == lb_tiles && out_count) *out_count = prefix + total;
       sm.tile_offset = prefix;
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (out == nullptr) return;  // count only
 
-  // Compact through LDS, then coalesced stores; positions at or past the
-  // destination's capacity are counted but not written.
-  const size_t base = sm.tile_offset;
-  if (base >= out_cap) return;  // uniform: the whole tile lies past the end
-  const uint32_t keep = static_cast<uint32_t>(std::min<size_t>(tile_count, out_cap - base));
-  __syncthreads();
-  {
-    uint32_t o = excl;
+  // Compact through LDS, then coalesced stores, one sub-tile at a time;
+  // positions at or past the destination's capacity are counted but not
+  // written.
+  size_t base = sm.tile_offset;
 #pragma unroll
-    for (int k = 0; k < ITEMS; ++k) {
-      if (mask & (1u << k)) {
-        sm.keys[o] = outk[k];
-        if constexpr (PAIRS) sm.vals[o] = outv_reg[k];
-        ++o;
+  for (int s = 0; s < SUB; ++s) {
+    const SubTile<K, VS, ITEMS, PAIRS> &r = sub[s];
+    if (base >= out_cap) return;  // uniform: the rest lies past the end
+    const uint32_t keep = static_cast<uint32_t>(std::min<size_t>(r.count, out_cap - base));
+    if (s > 0) lds_barrier();  // the previous sub-tile's stores have read the buffer
+    {
+      uint32_t o = r.excl;
+#pragma unroll
+      for (int k = 0; k < ITEMS; ++k) {
+        if (r.mask & (1u << k)) {
+          sm.keys[o] = r.outk[k];
+          if constexpr (PAIRS) sm.vals[o] = r.outv[k];
+          ++o;
+        }
       }
     }
-  }
-  __syncthreads();
-  constexpr int STORE = (Smem::CAP + THREADS - 1) / THREADS;
+    lds_barrier();
+    constexpr int STORE = (Smem::CAP + THREADS - 1) / THREADS;
 #pragma unroll
-  for (int k = 0; k < STORE; ++k) {
-    const uint32_t i = uint32_t(k) * THREADS + tid;
-    if (i < keep) {
-      out[base + i] = sm.keys[i];
-      if constexpr (PAIRS) outv[base + i] = sm.vals[i];
+    for (int k = 0; k < STORE; ++k) {
+      const uint32_t i = uint32_t(k) * THREADS + tid;
+      if (i < keep) {
+        out[base + i] = sm.keys[i];
+        if constexpr (PAIRS) outv[base + i] = sm.vals[i];
+      }
     }
+    base += r.count;
   }
 }
 
@@ -443,7 +501,7 @@ struct SetArgs {
 };
 
 struct Layout {
-  size_t tiles = 0, groups = 0;
+  size_t tiles = 0, lb_tiles = 0, groups = 0;  // partition tiles, look-back tiles
   size_t splits = 0, desc = 0, gagg = 0, ginc = 0, ticket = 0, total = 0;
 };
 
@@ -453,12 +511,14 @@ Layout layout(size_t na, size_t nb) {
   const size_t total = na + nb;
   constexpr size_t TILE = tile_items<K, V>();
   l.tiles = total ? (total + TILE - 1) / TILE : 1;  // an empty input still reports its count
-  l.groups = (l.tiles + GROUP - 1) / GROUP;
+  constexpr size_t SUB = sub_tiles_for<K, V>();
+  l.lb_tiles = (l.tiles + SUB - 1) / SUB;
+  l.groups = (l.lb_tiles + GROUP - 1) / GROUP;
   size_t off = 0;
   l.splits = off;
   off += align_up((l.tiles + 1) * 2 * sizeof(uint64_t), 256);
   l.desc = off;
-  off += l.tiles * sizeof(uint64_t);
+  off += l.lb_tiles * sizeof(uint64_t);
   l.gagg = off;
   off += l.groups * sizeof(uint64_t);
   l.ginc = off;
@@ -472,6 +532,7 @@ Layout layout(size_t na, size_t nb) {
 template <class K, class V, class Cmp, int OP>
 rccl_hip_status run_op(const SetArgs &s) {
   constexpr int ITEMS = items_for<K, V>();
+  constexpr int SUB = sub_tiles_for<K, V>();
   constexpr size_t TILE = tile_items<K, V>();
   const Layout l = layout<K, V>(s.na, s.nb);
   if (!s.ws || s.ws_bytes < l.total)
@@ -484,13 +545,13 @@ rccl_hip_status run_op(const SetArgs &s) {
   uint64_t *ginc = reinterpret_cast<uint64_t *>(ws + l.ginc);
   uint64_t *ticket = reinterpret_cast<uint64_t *>(ws + l.ticket);
   // Descriptors, group words and the ticket are contiguous.
-  const size_t state_words = lookback::state_words(l.tiles);
+  const size_t state_words = lookback::state_words(l.lb_tiles);
   uint32_t nx = 1;
   RCCL_HIP_TRY(tile_order(&nx));
   if (nx == XCDS)
     RCCL_HIP_TRY(check_xcd_rows(
-        s.arith ? reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, true>)
-                : reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, false>),
+        s.arith ? reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, SUB, true>)
+                : reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, SUB, false>),
         THREADS, XCD_RUN, "set tile does not fit on the device"));
   {
     KernelTimer t("set_clear", s.stream, state_words);
@@ -499,7 +560,8 @@ rccl_hip_status run_op(const SetArgs &s) {
   }
   RCCL_HIP_TRY(check_launch("set clear"));
   const dim3 pgrid(static_cast<uint32_t>((l.tiles + 1 + 255) / 256));
-  const dim3 tgrid(static_cast<uint32_t>(nx == XCDS ? xcd_order_grid(l.tiles, XCD_RUN) : l.tiles));
+  const dim3 tgrid(
+      static_cast<uint32_t>(nx == XCDS ? xcd_order_grid(l.lb_tiles, XCD_RUN) : l.lb_tiles));
   const K *a = static_cast<const K *>(s.a);
   const K *b = static_cast<const K *>(s.b);
   const V *av = static_cast<const V *>(s.av);
@@ -521,8 +583,8 @@ rccl_hip_status run_op(const SetArgs &s) {
       RCCL_HIP_TRY(check_launch("set partition"));
       {
         KernelTimer t("set_tile", s.stream, s.na + s.nb);
-        tile_kernel<K, V, Cmp, OP, ITEMS, true><<<tgrid, THREADS, 0, s.stream>>>(
-            a, av, b, bv, splits, l.tiles, out, outv, s.out_cap, s.out_count, desc, gagg, ginc,
+        tile_kernel<K, V, Cmp, OP, ITEMS, SUB, true><<<tgrid, THREADS, 0, s.stream>>>(
+            a, av, b, bv, splits, l.tiles, l.lb_tiles, out, outv, s.out_cap, s.out_count, desc, gagg, ginc,
             ticket, nx, ar, br);
       }
       return check_launch("set tile");
@@ -539,8 +601,8 @@ rccl_hip_status run_op(const SetArgs &s) {
   RCCL_HIP_TRY(check_launch("set partition"));
   {
     KernelTimer t("set_tile", s.stream, s.na + s.nb);
-    tile_kernel<K, V, Cmp, OP, ITEMS, false><<<tgrid, THREADS, 0, s.stream>>>(
-        a, av, b, bv, splits, l.tiles, out, outv, s.out_cap, s.out_count, desc, gagg, ginc,
+    tile_kernel<K, V, Cmp, OP, ITEMS, SUB, false><<<tgrid, THREADS, 0, s.stream>>>(
+        a, av, b, bv, splits, l.tiles, l.lb_tiles, out, outv, s.out_cap, s.out_count, desc, gagg, ginc,
         ticket, nx, Arith<K>{}, Arith<K>{});
   }
   return check_launch("set tile");
