@@ -84,51 +84,10 @@ partition_kernel(const K *__restrict__ a, size_t na, const K *__restrict__ b, si
                                       [&](size_t j) { return b[j]; }, nb, diag, Cmp{});
 }
 
-// ---------------------------------------------------------------------------
-// Sampled partition (integer keys, large merges). Every probe of a plain
-// merge-path search over HBM fetches its own random line, and neighbouring
-// searches share none. Here the top levels go to a shared sample instead:
-//   sample_kernel   for every SAMPLE-th item a_k = A[k * SAMPLE], m_k = the
-//                   number of sampled B items B[m * SAMPLE] strictly before it
-//                   (a search over the sampled positions, which stay in L2)
-//   partition       a_k's merged position is posA(k*S) = k*S + #{B < a_k},
-//                   and #{B < a_k} lies in [(m_k - 1)*S + 1, m_k*S] (or is 0
-//                   when m_k = 0): bounds L_k <= posA <= U_k. The A split of
-//                   diagonal d is i* = #{i : posA(i) < d}, so U_k < d gives
-//                   i* > k*S and L_k >= d gives i* <= k*S. With kk the first
-//                   sample whose U reaches d, i* > (kk - 1)*S; and since
-//                   L_{k+1} > U_k whenever m_k > 0, sample kk or kk + 1 has
-//                   L >= d, which caps i* at most 2*S above the lower bound.
-//                   The merge-path search then runs in that window only.
-// Floats keep the plain search: NaN makes the order partial.
-// ---------------------------------------------------------------------------
-#ifndef RCCL_MERGE_SAMPLE
-#define RCCL_MERGE_SAMPLE 2048
-#endif
-constexpr size_t SAMPLE = RCCL_MERGE_SAMPLE;
+// Sampled partition (integer keys, from SAMPLED_MIN_TILES tiles):
+// ordering::merge_sample_kernel, then each tile boundary's split from
+// ordering::sampled_merge_path.
 constexpr size_t SAMPLED_MIN_TILES = 512;
-
-template <class K>
-constexpr bool sampled_partition_for() {
-  return std::is_integral<K>::value;
-}
-
-template <class K, class Cmp>
-__global__ void __launch_bounds__(256)
-sample_kernel(const K *__restrict__ a, size_t na, const K *__restrict__ b, size_t nb,
-              uint32_t *__restrict__ m_out) {
-  const size_t k = size_t(blockIdx.x) * 256 + threadIdx.x;
-  const size_t ka = (na + SAMPLE - 1) / SAMPLE, kb = (nb + SAMPLE - 1) / SAMPLE;
-  if (k >= ka) return;
-  const K x = a[k * SAMPLE];
-  const Cmp less{};
-  size_t lo = 0, hi = kb;  // first sampled B position not before x
-  while (lo < hi) {
-    const size_t mid = lo + (hi - lo) / 2;
-    if (less(b[mid * SAMPLE], x)) lo = mid + 1; else hi = mid;
-  }
-  m_out[k] = static_cast<uint32_t>(lo);
-}
 
 template <class K, class Cmp>
 __global__ void __launch_bounds__(256)
@@ -138,31 +97,8 @@ sampled_partition_kernel(const K *__restrict__ a, size_t na, const K *__restrict
   const size_t t = size_t(blockIdx.x) * 256 + threadIdx.x;
   if (t >= count) return;
   const size_t d = std::min(t * tile, na + nb);
-  const size_t ka = (na + SAMPLE - 1) / SAMPLE;
-  auto upper = [&](size_t k) { return k * SAMPLE + std::min(nb, size_t(m[k]) * SAMPLE); };
-  auto lower = [&](size_t k) {
-    return k * SAMPLE + (m[k] ? (size_t(m[k]) - 1) * SAMPLE + 1 : size_t(0));
-  };
-  size_t lo = 0, hi = ka;  // kk: first sample with upper(k) >= d
-  while (lo < hi) {
-    const size_t mid = lo + (hi - lo) / 2;
-    if (upper(mid) < d) lo = mid + 1; else hi = mid;
-  }
-  const size_t kk = lo;
-  size_t ilo = d > nb ? d - nb : 0;
-  size_t ihi = d < na ? d : na;
-  if (kk > 0) ilo = std::max(ilo, (kk - 1) * SAMPLE + 1);
-  if (kk < ka) {
-    if (lower(kk) >= d) ihi = std::min(ihi, kk * SAMPLE);
-    else if (kk + 1 < ka) ihi = std::min(ihi, (kk + 1) * SAMPLE);
-  }
-  // Merge-path search (ordering::merge_path) restricted to [ilo, ihi].
-  const Cmp less{};
-  while (ilo < ihi) {
-    const size_t mid = ilo + (ihi - ilo) / 2;
-    if (less(b[d - 1 - mid], a[mid])) ihi = mid; else ilo = mid + 1;
-  }
-  splits[t] = ilo;
+  splits[t] = ordering::sampled_merge_path<K>([&](size_t x) { return a[x]; }, na,
+                                              [&](size_t x) { return b[x]; }, nb, d, m, Cmp{});
 }
 
 // LDS layout of one merge tile.
@@ -285,18 +221,18 @@ struct MergeArgs {
 template <class K, class V>
 bool use_sampled(size_t na, size_t nb) {
   const size_t tiles = (na + nb + call_tile_items<K, V>() - 1) / call_tile_items<K, V>();
-  return sampled_partition_for<K>() && na > 0 && nb > 0 && tiles >= SAMPLED_MIN_TILES;
+  return ordering::sampled_partition_for<K>() && na > 0 && nb > 0 && tiles >= SAMPLED_MIN_TILES;
 }
 
 // Splits (one u64 per tile boundary), then the samples' m_k (one u32 per
-// SAMPLE items of A) when the sampled partition runs.
+// MERGE_SAMPLE items of A) when the sampled partition runs.
 template <class K, class V>
 size_t workspace_bytes(size_t na, size_t nb) {
   const size_t total = na + nb;
   if (total == 0) return 0;
   const size_t tiles = (total + call_tile_items<K, V>() - 1) / call_tile_items<K, V>();
   size_t bytes = align_up((tiles + 1) * sizeof(uint64_t), 256);
-  if (use_sampled<K, V>(na, nb)) bytes += align_up((na + SAMPLE - 1) / SAMPLE * 4, 256);
+  if (use_sampled<K, V>(na, nb)) bytes += align_up(ordering::merge_samples(na) * 4, 256);
   return bytes;
 }
 
@@ -315,11 +251,12 @@ rccl_hip_status run_merge(const MergeArgs &m) {
   if (use_sampled<K, V>(m.na, m.nb)) {
     uint32_t *samples = reinterpret_cast<uint32_t *>(static_cast<unsigned char *>(m.ws) +
                                                      align_up((tiles + 1) * sizeof(uint64_t), 256));
-    const size_t ka = (m.na + SAMPLE - 1) / SAMPLE;
+    const size_t ka = ordering::merge_samples(m.na);
     {
       KernelTimer t("merge_sample", m.stream, ka);
-      sample_kernel<K, Cmp><<<dim3(static_cast<uint32_t>((ka + 255) / 256)), 256, 0, m.stream>>>(
-          static_cast<const K *>(m.a), m.na, static_cast<const K *>(m.b), m.nb, samples);
+      ordering::merge_sample_kernel<K, Cmp>
+          <<<dim3(static_cast<uint32_t>((ka + 255) / 256)), 256, 0, m.stream>>>(
+              static_cast<const K *>(m.a), m.na, static_cast<const K *>(m.b), m.nb, samples);
     }
     RCCL_HIP_TRY(check_launch("merge sample"));
     KernelTimer t("merge_partition", m.stream, tiles + 1);

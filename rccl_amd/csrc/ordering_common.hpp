@@ -3,6 +3,7 @@
 // a runtime (key kind, order, value width) onto compile-time instantiations.
 #pragma once
 
+#include <algorithm>
 #include <limits>
 #include <type_traits>
 
@@ -98,6 +99,86 @@ __device__ __forceinline__ size_t merge_path(ReadA a, size_t na, ReadB b, size_t
       lo = mid + 1;
   }
   return lo;
+}
+
+// ---------------------------------------------------------------------------
+// Sampled merge path (integer keys). Every probe of a plain merge-path search
+// over HBM fetches its own random line, and neighbouring searches share none.
+// Here the top levels go to a shared sample instead:
+//   merge_sample_kernel  for every MERGE_SAMPLE-th item a_k = A[k*S], m_k =
+//                        the number of sampled B items B[m*S] strictly before
+//                        it (a search over the sampled positions, which stay
+//                        in L2)
+//   sampled_merge_path   a_k's merged position is posA(k*S) = k*S + #{B < a_k},
+//                        and #{B < a_k} lies in [(m_k - 1)*S + 1, m_k*S] (or
+//                        is 0 when m_k = 0): bounds L_k <= posA <= U_k. The A
+//                        split of diagonal d is i* = #{i : posA(i) < d}, so
+//                        U_k < d gives i* > k*S and L_k >= d gives i* <= k*S.
+//                        With kk the first sample whose U reaches d,
+//                        i* > (kk - 1)*S; and since L_{k+1} > U_k whenever
+//                        m_k > 0, sample kk or kk + 1 has L >= d, which caps
+//                        i* at most 2*S above the lower bound. The merge-path
+//                        search then runs in that window only.
+// Floats keep the plain search: NaN makes the order partial.
+// ---------------------------------------------------------------------------
+#ifndef RCCL_MERGE_SAMPLE
+#define RCCL_MERGE_SAMPLE 2048
+#endif
+constexpr size_t MERGE_SAMPLE = RCCL_MERGE_SAMPLE;
+
+template <class K>
+constexpr bool sampled_partition_for() {
+  return std::is_integral<K>::value;
+}
+
+// Samples of an A of `na` items (entries of the m array).
+__host__ __device__ inline size_t merge_samples(size_t na) { return (na + MERGE_SAMPLE - 1) / MERGE_SAMPLE; }
+
+template <class K, class Cmp>
+__global__ void __launch_bounds__(256)
+merge_sample_kernel(const K *__restrict__ a, size_t na, const K *__restrict__ b, size_t nb,
+                    uint32_t *__restrict__ m_out) {
+  const size_t k = size_t(blockIdx.x) * 256 + threadIdx.x;
+  const size_t ka = merge_samples(na), kb = merge_samples(nb);
+  if (k >= ka) return;
+  const K x = a[k * MERGE_SAMPLE];
+  const Cmp less{};
+  size_t lo = 0, hi = kb;  // first sampled B position not before x
+  while (lo < hi) {
+    const size_t mid = lo + (hi - lo) / 2;
+    if (less(b[mid * MERGE_SAMPLE], x)) lo = mid + 1; else hi = mid;
+  }
+  m_out[k] = static_cast<uint32_t>(lo);
+}
+
+// merge_path of diagonal d, searched in the window the samples allow.
+template <class K, class Cmp, class ReadA, class ReadB>
+__device__ __forceinline__ size_t sampled_merge_path(ReadA a, size_t na, ReadB b, size_t nb,
+                                                     size_t d, const uint32_t *__restrict__ m,
+                                                     Cmp less) {
+  constexpr size_t S = MERGE_SAMPLE;
+  const size_t ka = merge_samples(na);
+  auto upper = [&](size_t k) { return k * S + std::min(nb, size_t(m[k]) * S); };
+  auto lower = [&](size_t k) { return k * S + (m[k] ? (size_t(m[k]) - 1) * S + 1 : size_t(0)); };
+  size_t lo = 0, hi = ka;  // kk: first sample with upper(k) >= d
+  while (lo < hi) {
+    const size_t mid = lo + (hi - lo) / 2;
+    if (upper(mid) < d) lo = mid + 1; else hi = mid;
+  }
+  const size_t kk = lo;
+  size_t ilo = d > nb ? d - nb : 0;
+  size_t ihi = d < na ? d : na;
+  if (kk > 0) ilo = std::max(ilo, (kk - 1) * S + 1);
+  if (kk < ka) {
+    if (lower(kk) >= d) ihi = std::min(ihi, kk * S);
+    else if (kk + 1 < ka) ihi = std::min(ihi, (kk + 1) * S);
+  }
+  // merge_path restricted to [ilo, ihi].
+  while (ilo < ihi) {
+    const size_t mid = ilo + (ihi - ilo) / 2;
+    if (less(b(d - 1 - mid), a(mid))) ihi = mid; else ilo = mid + 1;
+  }
+  return ilo;
 }
 
 // 32-bit variant for LDS-resident slices.

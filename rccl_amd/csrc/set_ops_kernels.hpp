@@ -135,10 +135,11 @@ __device__ __forceinline__ size_t gallop_up(R r, size_t lo, size_t hi, Pred afte
 // kernel over HBM, where each probe is a dependent round trip and runs of
 // equal keys are usually short: 60 -> 36 us per C5 operation); otherwise by
 // binary search (the tile kernel in LDS, where galloping measured no faster).
+// balanced_path_at starts from the merge-path split i of the diagonal.
 template <bool GALLOP, class K, class Cmp, class RA, class RB>
-__device__ __forceinline__ void balanced_path(RA a, size_t na, RB b, size_t nb, size_t diag,
-                                              Cmp less, size_t &out_i, size_t &out_j) {
-  size_t i = ordering::merge_path<K>(a, na, b, nb, diag, less);
+__device__ __forceinline__ void balanced_path_at(RA a, size_t na, RB b, size_t nb, size_t diag,
+                                                 size_t i, Cmp less, size_t &out_i,
+                                                 size_t &out_j) {
   const size_t j = diag - i;
   size_t star = 0;
   // No A item before the split and no B item before it is equal to B[j]:
@@ -187,34 +188,46 @@ __device__ __forceinline__ void balanced_path(RA a, size_t na, RB b, size_t nb, 
   out_j = diag - i + star;
 }
 
-template <class K, class Cmp, bool ARITH>
+template <bool GALLOP, class K, class Cmp, class RA, class RB>
+__device__ __forceinline__ void balanced_path(RA a, size_t na, RB b, size_t nb, size_t diag,
+                                              Cmp less, size_t &out_i, size_t &out_j) {
+  balanced_path_at<GALLOP, K>(a, na, b, nb, diag, ordering::merge_path<K>(a, na, b, nb, diag, less),
+                              less, out_i, out_j);
+}
+
+// Also zeroes the tile kernel's look-back state (descriptors, group words and
+// the ticket: `state_words` words at `state`), which no earlier launch of the
+// call touches, so no separate clearing launch is needed.
+// With SAMPLED, the merge-path split comes from the samples of
+// ordering::merge_sample_kernel (m) before the balanced path adjusts it.
+template <class K, class Cmp, bool ARITH, bool SAMPLED>
 __global__ void __launch_bounds__(256)
 partition_kernel(const K *__restrict__ a, size_t na, const K *__restrict__ b, size_t nb,
                  size_t tile, size_t count, uint64_t *__restrict__ splits, Arith<K> ar,
-                 Arith<K> br) {
+                 Arith<K> br, uint64_t *__restrict__ state, size_t state_words,
+                 const uint32_t *__restrict__ m) {
   const size_t t = size_t(blockIdx.x) * 256 + threadIdx.x;
+  for (size_t w = t; w < state_words; w += size_t(gridDim.x) * 256) state[w] = 0;
   if (t >= count) return;
   const size_t diag = std::min(t * tile, na + nb);
   size_t i, j;
-  if constexpr (ARITH)
+  if constexpr (ARITH) {
     balanced_path<true, K>([&](size_t x) { return arith_at(ar, x); }, na,
-                     [&](size_t x) { return arith_at(br, x); }, nb, diag, Cmp{}, i, j);
-  else
-    balanced_path<true, K>([&](size_t x) { return a[x]; }, na,
-                                             [&](size_t x) { return b[x]; }, nb, diag, Cmp{}, i,
-                                             j);
+                           [&](size_t x) { return arith_at(br, x); }, nb, diag, Cmp{}, i, j);
+  } else {
+    auto ra = [&](size_t x) { return a[x]; };
+    auto rb = [&](size_t x) { return b[x]; };
+    if constexpr (SAMPLED)
+      balanced_path_at<true, K>(ra, na, rb, nb, diag,
+                                ordering::sampled_merge_path<K>(ra, na, rb, nb, diag, m, Cmp{}),
+                                Cmp{}, i, j);
+    else
+      balanced_path<true, K>(ra, na, rb, nb, diag, Cmp{}, i, j);
+  }
   splits[2 * t] = i;
   splits[2 * t + 1] = j;
 }
 
-// Zero the look-back state (tile descriptors, group aggregates and inclusive
-// prefixes) before a launch (one copy per translation unit).
-namespace {
-__global__ void __launch_bounds__(256) clear_kernel(uint64_t *p, size_t words) {
-  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < words; i += size_t(gridDim.x) * 256)
-    p[i] = 0;
-}
-} // namespace
 
 template <class K, class V, int ITEMS>
 struct TileSmem {
@@ -502,8 +515,14 @@ struct SetArgs {
 
 struct Layout {
   size_t tiles = 0, lb_tiles = 0, groups = 0;  // partition tiles, look-back tiles
-  size_t splits = 0, desc = 0, gagg = 0, ginc = 0, ticket = 0, total = 0;
+  size_t splits = 0, desc = 0, gagg = 0, ginc = 0, ticket = 0, samples = 0, total = 0;
+  bool sampled = false;  // integer keys from SAMPLED_MIN_TILES partition tiles
 };
+
+// The sampled merge-path partition serves inputs of at least this many
+// partition tiles (integer keys; arithmetic ranges compute their items and
+// keep the plain search).
+constexpr size_t SAMPLED_MIN_TILES = 512;
 
 template <class K, class V>
 Layout layout(size_t na, size_t nb) {
@@ -525,6 +544,13 @@ Layout layout(size_t na, size_t nb) {
   off += l.groups * sizeof(uint64_t);
   l.ticket = off;
   off += sizeof(uint64_t);
+  l.sampled = ordering::sampled_partition_for<K>() && na > 0 && nb > 0 &&
+              l.tiles >= SAMPLED_MIN_TILES;
+  if (l.sampled) {
+    off = align_up(off, 256);
+    l.samples = off;
+    off += ordering::merge_samples(na) * sizeof(uint32_t);
+  }
   l.total = align_up(off, 256);
   return l;
 }
@@ -553,12 +579,6 @@ rccl_hip_status run_op(const SetArgs &s) {
         s.arith ? reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, SUB, true>)
                 : reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, SUB, false>),
         THREADS, XCD_RUN, "set tile does not fit on the device"));
-  {
-    KernelTimer t("set_clear", s.stream, state_words);
-    clear_kernel<<<dim3(static_cast<uint32_t>(std::min<size_t>((state_words + 255) / 256, 1024))),
-                   256, 0, s.stream>>>(desc, state_words);
-  }
-  RCCL_HIP_TRY(check_launch("set clear"));
   const dim3 pgrid(static_cast<uint32_t>((l.tiles + 1 + 255) / 256));
   const dim3 tgrid(
       static_cast<uint32_t>(nx == XCDS ? xcd_order_grid(l.lb_tiles, XCD_RUN) : l.lb_tiles));
@@ -577,8 +597,8 @@ rccl_hip_status run_op(const SetArgs &s) {
       std::memcpy(&br.step, &s.b_step, sizeof(K));
       {
         KernelTimer t("set_partition", s.stream, l.tiles + 1);
-        partition_kernel<K, Cmp, true><<<pgrid, 256, 0, s.stream>>>(a, s.na, b, s.nb, TILE,
-                                                                     l.tiles + 1, splits, ar, br);
+        partition_kernel<K, Cmp, true, false><<<pgrid, 256, 0, s.stream>>>(
+            a, s.na, b, s.nb, TILE, l.tiles + 1, splits, ar, br, desc, state_words, nullptr);
       }
       RCCL_HIP_TRY(check_launch("set partition"));
       {
@@ -592,11 +612,28 @@ rccl_hip_status run_op(const SetArgs &s) {
       return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "arithmetic range key kind");
     }
   }
+  uint32_t *m = l.sampled ? reinterpret_cast<uint32_t *>(ws + l.samples) : nullptr;
+  if (l.sampled) {
+    const size_t ka = ordering::merge_samples(s.na);
+    {
+      KernelTimer t("set_sample", s.stream, ka);
+      ordering::merge_sample_kernel<K, Cmp>
+          <<<dim3(static_cast<uint32_t>((ka + 255) / 256)), 256, 0, s.stream>>>(a, s.na, b, s.nb,
+                                                                               m);
+    }
+    RCCL_HIP_TRY(check_launch("set sample"));
+  }
   {
     KernelTimer t("set_partition", s.stream, l.tiles + 1);
-    partition_kernel<K, Cmp, false><<<pgrid, 256, 0, s.stream>>>(a, s.na, b, s.nb, TILE,
-                                                                  l.tiles + 1, splits, Arith<K>{},
-                                                                  Arith<K>{});
+    if (l.sampled) {
+      partition_kernel<K, Cmp, false, true><<<pgrid, 256, 0, s.stream>>>(
+          a, s.na, b, s.nb, TILE, l.tiles + 1, splits, Arith<K>{}, Arith<K>{}, desc, state_words,
+          m);
+    } else {
+      partition_kernel<K, Cmp, false, false><<<pgrid, 256, 0, s.stream>>>(
+          a, s.na, b, s.nb, TILE, l.tiles + 1, splits, Arith<K>{}, Arith<K>{}, desc, state_words,
+          nullptr);
+    }
   }
   RCCL_HIP_TRY(check_launch("set partition"));
   {

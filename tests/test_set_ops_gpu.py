@@ -244,3 +244,48 @@ def test_set_c5_scaled(exec_):
         k, _, n = _run(exec_, op, a, b)
         want = oracle.set_op(op, "u64", a, b)
         assert n == want.size and np.array_equal(k[:n], want), op
+
+
+def _sampled_set_inputs(kind, descending):
+    """Sorted multisets of at least 512 partition tiles (the sampled
+    partition), with the shapes that stress the sample bracket and the
+    balanced path's equal-key runs: heavy duplicates (runs spanning many
+    tiles), uniform keys, one side far shorter, all keys equal, and disjoint
+    ranges either way round."""
+    dt = np.dtype({"u8": np.uint8, "u32": np.uint32, "i64": np.int64}[kind])
+    n = (1 << 22) + 5
+    info = np.iinfo(dt)
+
+    def rnd(size, seed, distinct=None):
+        raw = workloads.hash_range(seed, size)
+        if distinct is not None:
+            raw = raw % np.uint64(distinct)
+        v = raw.astype(dt) if dt.kind == "u" else (raw >> np.uint64(1)).astype(dt)
+        s = np.sort(v, kind="stable")
+        return s[::-1].copy() if descending else s
+
+    yield "dups", rnd(n, 61, 37), rnd(n - 9, 62, 37)
+    yield "uniform", rnd(n, 63), rnd(n + 2047, 64)
+    yield "short_b", rnd(2 * n, 65, 1000), rnd(3001, 66, 1000)
+    yield "all_equal", np.full(n, 5, dt), np.full(n + 3, 5, dt)
+    lo, hi = np.full(n, info.min, dt), np.full(n + 7, info.max, dt)
+    first, second = (hi, lo) if descending else (lo, hi)
+    yield "disjoint", first, second
+    yield "disjoint_reversed", second, first
+
+
+@pytest.mark.parametrize("kind", ["u8", "u32", "i64"])
+@pytest.mark.parametrize("descending", [False, True])
+def test_set_sampled_partition_vs_oracle(exec_, kind, descending):
+    for idx, (name, a, b) in enumerate(_sampled_set_inputs(kind, descending)):
+        for op in OPS:
+            if idx == 1 and op in ("union", "symmetric_difference"):
+                av = np.arange(a.size, dtype=np.uint32)
+                bv = np.arange(b.size, dtype=np.uint32) | np.uint32(1 << 31)
+                k, v, n = _run(exec_, op, a, b, av, bv, descending)
+                wk, wv = oracle.set_op(op, kind, a, b, av, bv, descending)
+                assert n == wk.size and np.array_equal(v[:n], wv), (kind, name, op)
+            else:
+                k, _, n = _run(exec_, op, a, b, descending=descending)
+                wk = oracle.set_op(op, kind, a, b, descending=descending)
+            assert n == wk.size and np.array_equal(k[:n], wk), (kind, name, op, descending)
