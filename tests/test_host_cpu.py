@@ -444,3 +444,33 @@ def test_radix_configure_validates(lib):
         for order in _abi.TILE_ORDER.values():
             assert lib.rccl_hip_radix_configure(ranking, order) == 0
     assert lib.rccl_hip_radix_configure(0, 0) == 0
+
+
+def test_sampled_partition_workspaces(lib):
+    """From 512 tiles, integer-key merges and set operations hold one u32
+    sample count per 2,048 items of the first input beside the tile splits;
+    below that, and for float keys, the workspace holds the splits (and the
+    set operations' look-back state) alone. Exact sizes, worked out by hand
+    from the layout: 256-byte aligned sections."""
+    merge = lambda na, nb, key=0: _abi.workspace_bytes(
+        "rccl_hip_merge_workspace_bytes", key, 4, na, nb)
+    # u32 keys + u32 values: 2,048-item tiles. 2^19 items = 256 tiles: splits
+    # only, (256 + 1) * 8 B -> 2,304 B.
+    assert merge(1 << 18, 1 << 18) == 2304
+    # 2^23 items = 4,096 tiles: splits 4,097 * 8 B -> 33,024 B, plus 2,048
+    # sample counts of 4 B (2^22 / 2,048) -> 41,216 B.
+    assert merge(1 << 22, 1 << 22) == 41216
+    # f32 keys keep the plain search: splits only.
+    assert merge(1 << 22, 1 << 22, key=2) == 33024
+    setop = lambda na, nb, key: _abi.workspace_bytes(
+        "rccl_hip_set_op_workspace_bytes", 0, key, 0, na, nb)
+    # u32 keys only: 8,192-item partition tiles, two per look-back tile,
+    # groups of 64 look-back tiles. 2^21 items = 256 tiles: splits
+    # 257 * 16 B -> 4,352 B, then 128 descriptors, 2 + 2 group words and the
+    # ticket (1,064 B) -> 5,632 B.
+    assert setop(1 << 20, 1 << 20, 0) == 5632
+    # 2^23 items = 1,024 tiles: splits 1,025 * 16 B -> 16,640 B, 512
+    # descriptors, 8 + 8 group words, the ticket -> 20,872 B, aligned to
+    # 20,992 B, plus 2,048 sample counts -> 29,184 B; f32 keys: 20,992 B.
+    assert setop(1 << 22, 1 << 22, 0) == 29184
+    assert setop(1 << 22, 1 << 22, 2) == 20992
