@@ -43,14 +43,26 @@ constexpr uint32_t XCD_RUN = RCCL_SET_XCD_RUN;  // tiles per XCD run (xcd_order_
 
 enum Op : int { UNION = 0, INTERSECTION = 1, DIFFERENCE = 2, SYMMETRIC_DIFFERENCE = 3 };
 
-template <class K, class V>
+// Union and symmetric difference of 8-byte keys emit from both inputs: their
+// outputs, kept in registers for two partition tiles, fit the 128-register
+// budget without spilling at one item fewer per thread.
+#ifndef RCCL_SET_ITEMS_8B_BOTH
+#define RCCL_SET_ITEMS_8B_BOTH 15
+#endif
+template <class K, class V, int OP>
 constexpr int items_for() {
-  constexpr size_t bytes = sizeof(K) + (std::is_same<V, NoValue>::value ? 0 : sizeof(V));
+  constexpr bool keys_only = std::is_same<V, NoValue>::value;
+  constexpr size_t bytes = sizeof(K) + (keys_only ? 0 : sizeof(V));
+  if constexpr (keys_only && sizeof(K) == 8 && (OP == UNION || OP == SYMMETRIC_DIFFERENCE))
+    return RCCL_SET_ITEMS_8B_BOTH;
   return bytes <= 8 ? RCCL_SET_ITEMS_8B : (bytes <= 16 ? 12 : 8);
 }
+// The fewest items per thread over the four operations: the most partition
+// tiles, which sizes a workspace that serves every operation.
 template <class K, class V>
-constexpr size_t tile_items() {
-  return size_t(THREADS) * items_for<K, V>();
+constexpr int min_items_for() {
+  return std::min(std::min(items_for<K, V, UNION>(), items_for<K, V, INTERSECTION>()),
+                  std::min(items_for<K, V, DIFFERENCE>(), items_for<K, V, SYMMETRIC_DIFFERENCE>()));
 }
 // Partition tiles per block (and per look-back tile): two for keys only,
 // whose two register sets of outputs fit; one where values double them.
@@ -524,11 +536,14 @@ struct Layout {
 // keep the plain search).
 constexpr size_t SAMPLED_MIN_TILES = 512;
 
-template <class K, class V>
+// Workspace layout for partition tiles of ITEMS items per thread. Fewer items
+// give more tiles and no smaller a section, so the layout at min_items_for
+// bounds every operation's.
+template <class K, class V, int ITEMS>
 Layout layout(size_t na, size_t nb) {
   Layout l;
   const size_t total = na + nb;
-  constexpr size_t TILE = tile_items<K, V>();
+  constexpr size_t TILE = size_t(THREADS) * ITEMS;
   l.tiles = total ? (total + TILE - 1) / TILE : 1;  // an empty input still reports its count
   constexpr size_t SUB = sub_tiles_for<K, V>();
   l.lb_tiles = (l.tiles + SUB - 1) / SUB;
@@ -557,10 +572,10 @@ Layout layout(size_t na, size_t nb) {
 
 template <class K, class V, class Cmp, int OP>
 rccl_hip_status run_op(const SetArgs &s) {
-  constexpr int ITEMS = items_for<K, V>();
+  constexpr int ITEMS = items_for<K, V, OP>();
   constexpr int SUB = sub_tiles_for<K, V>();
-  constexpr size_t TILE = tile_items<K, V>();
-  const Layout l = layout<K, V>(s.na, s.nb);
+  constexpr size_t TILE = size_t(THREADS) * ITEMS;
+  const Layout l = layout<K, V, ITEMS>(s.na, s.nb);
   if (!s.ws || s.ws_bytes < l.total)
     return set_error(RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL, "set operation workspace", l.total,
                      s.ws_bytes);
@@ -659,6 +674,12 @@ struct KindRunner {
   }
 };
 
+// Workspace bytes for keys K and values V, whatever the operation.
+template <class K, class V>
+size_t bytes_v(size_t na, size_t nb) {
+  return layout<K, V, min_items_for<K, V>()>(na, nb).total;
+}
+
 #define RCCL_SET_DECLARE_KIND(NAME)                                                       \
   rccl_hip_status run_##NAME(const SetArgs &s, size_t value_bytes, bool descending);      \
   size_t bytes_##NAME(size_t na, size_t nb, size_t value_bytes);
@@ -687,12 +708,12 @@ RCCL_SET_DECLARE_KIND(f64)
   }                                                                                         \
   size_t bytes_##NAME(size_t na, size_t nb, size_t value_bytes) {                           \
     switch (value_bytes) {                                                                  \
-    case 0: return layout<KT, ordering::NoValue>(na, nb).total;                             \
-    case 1: return layout<KT, uint8_t>(na, nb).total;                                       \
-    case 2: return layout<KT, uint16_t>(na, nb).total;                                      \
-    case 4: return layout<KT, uint32_t>(na, nb).total;                                      \
-    case 8: return layout<KT, uint64_t>(na, nb).total;                                      \
-    default: return layout<KT, Value16>(na, nb).total;                                      \
+    case 0: return bytes_v<KT, ordering::NoValue>(na, nb);                                  \
+    case 1: return bytes_v<KT, uint8_t>(na, nb);                                            \
+    case 2: return bytes_v<KT, uint16_t>(na, nb);                                           \
+    case 4: return bytes_v<KT, uint32_t>(na, nb);                                           \
+    case 8: return bytes_v<KT, uint64_t>(na, nb);                                           \
+    default: return bytes_v<KT, Value16>(na, nb);                                           \
     }                                                                                       \
   }
 
