@@ -76,9 +76,19 @@ inline bool valid_value_bytes(size_t v) {
   return v == 0 || v == 1 || v == 2 || v == 4 || v == 8 || v == 16;
 }
 
-// Opaque value payloads moved alongside keys.
+// Opaque 16-byte value payloads moved alongside keys. Copies are one 16-byte
+// vector move: a defaulted copy of the struct becomes a byte copy that the
+// compiler leaves in scratch memory when it stages arrays of them between LDS
+// and registers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 struct alignas(16) Value16 {
-  uint32_t w[4];
+  u32x4 w;
+  Value16() = default;
+  __host__ __device__ Value16(const Value16 &o) : w(o.w) {}
+  __host__ __device__ Value16 &operator=(const Value16 &o) {
+    w = o.w;
+    return *this;
+  }
 };
 
 // ---------------------------------------------------------------------------

@@ -155,6 +155,13 @@ template <class Desc> struct LookbackBuf {
 #define RCCL_RADIX_XCD_RUN 8
 #endif
 constexpr int LOOKBACK = RCCL_RADIX_LOOKBACK_WINDOW;
+// Tile slots of the look-back window: half as many for 64-bit descriptors,
+// which keeps the window at the same registers (the wide window otherwise
+// pushes pair sorts past the register budget into scratch).
+template <class Desc>
+constexpr int lookback_window() {
+  return sizeof(Desc) == 8 ? (LOOKBACK + 1) / 2 : LOOKBACK;
+}
 constexpr int GROUP = RCCL_RADIX_LOOKBACK_GROUP;
 constexpr int GWIN = RCCL_RADIX_GROUP_WINDOW;
 constexpr uint32_t XCD_RUN = RCCL_RADIX_XCD_RUN;
@@ -427,9 +434,10 @@ inline size_t onesweep_grid(size_t tiles, uint32_t nx) {
 template <class Desc>
 __device__ __forceinline__ Desc lookback_consume(const LookbackBuf<Desc> &lbuf, uint32_t tile,
                                                  uint32_t group, uint32_t digit,
-                                                 Desc (&lb)[LOOKBACK], Desc (&gi)[GWIN],
-                                                 uint32_t (&ga)[GWIN]) {
+                                                 Desc (&lb)[lookback_window<Desc>()],
+                                                 Desc (&gi)[GWIN], uint32_t (&ga)[GWIN]) {
   using DI = DescInfo<Desc>;
+  constexpr int WIN = lookback_window<Desc>();
   const int gfirst = static_cast<int>(group) * GROUP;
   Desc excl = 0;
   bool done = tile == 0;
@@ -439,7 +447,7 @@ __device__ __forceinline__ Desc lookback_consume(const LookbackBuf<Desc> &lbuf, 
     int consumed = 0;
     bool stop = false;
 #pragma unroll
-    for (int w = 0; w < LOOKBACK; ++w) {
+    for (int w = 0; w < WIN; ++w) {
       if (!done && !stop) {
         const Desc v = t - w >= gfirst ? lb[w] : DI::BOUNDARY;
         const Desc flag = v >> DI::SHIFT;
@@ -486,7 +494,7 @@ __device__ __forceinline__ Desc lookback_consume(const LookbackBuf<Desc> &lbuf, 
     while (!done && t >= gfirst) {
       if (c == 0) __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-      for (int w = 0; w < LOOKBACK; ++w)
+      for (int w = 0; w < WIN; ++w)
         lb[w] = load_agent(&lbuf.tile[size_t(max(t - w, 0)) * BINS + digit]);
       c = eat_tiles();
     }
@@ -645,7 +653,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   const int gfirst = static_cast<int>(group) * GROUP;
   uint32_t count = 0, tile_inc = 0;
   uint32_t wc[WAVES];
-  Desc lb[LOOKBACK];
+  Desc lb[lookback_window<Desc>()];
   Desc gi[GWIN];
   uint32_t ga[GWIN];
   if (tid < BINS) {
@@ -660,7 +668,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     // Window loads are clamped to valid slots; slots outside the window are
     // masked when the window is consumed.
 #pragma unroll
-    for (int w = 0; w < LOOKBACK; ++w)
+    for (int w = 0; w < lookback_window<Desc>(); ++w)
       lb[w] = load_agent(
           &lbuf.tile[size_t(max(static_cast<int>(tile) - 1 - w, 0)) * BINS + tid]);
 #pragma unroll

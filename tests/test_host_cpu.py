@@ -474,3 +474,16 @@ def test_sampled_partition_workspaces(lib):
     # 20,992 B, plus 2,048 sample counts -> 29,184 B; f32 keys: 20,992 B.
     assert setop(1 << 22, 1 << 22, 0) == 29184
     assert setop(1 << 22, 1 << 22, 2) == 20992
+
+
+def test_radix_wide_descriptors_from_2pow30(lib):
+    """From 2^30 items the radix look-back descriptors are 64-bit (a digit's
+    prefix count no longer fits in 30 bits). u32 keys only: 512 x 34 = 17,408
+    items per tile, so 2^30 - 1 and 2^30 items both make 61,681 tiles in 3,856
+    groups of 16; the two look-back buffers each hold 61,681 x 256 tile
+    descriptors and 3,856 x 256 group prefixes, which grow by 4 bytes each:
+    2 x (61,681 + 3,856) x 256 x 4 = 134,219,776 bytes (every section already
+    256-byte aligned); nothing else changes."""
+    ws = lambda n: _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", 0, 0, n)
+    assert ws(1 << 30) - ws((1 << 30) - 1) == 134_219_776
+    assert ws((1 << 30) + 1) - ws(1 << 30) == 0  # the same tile count

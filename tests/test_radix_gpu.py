@@ -162,6 +162,29 @@ def test_pairs_narrow_domain(launch, value_dtype, descending):
     np.testing.assert_array_equal(gv, wv)
 
 
+@pytest.mark.parametrize("kind", ["u32", "i64"])
+@pytest.mark.parametrize("width", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("descending", [False, True])
+def test_pairs_every_value_width_multi_tile(launch, kind, width, descending):
+    """Every value width through the onesweep passes (100,003 items: several
+    tiles, a partial last one), including 16-byte values, whose payload
+    bytes are random so a mixed-up word would show. Keys are 10 bits wide
+    (ties in every tile); outputs are bit-exact with the oracle."""
+    dt = np.dtype(oracle.KIND_DTYPES[kind])
+    n = 100_003
+    raw = workloads.hash_range(4242 + width, n)
+    keys = (raw >> np.uint64(54)).astype(np.dtype(f"u{dt.itemsize}")).view(dt)
+    if width == 16:
+        vals = workloads.hash_range(77, 2 * n).view(np.dtype((np.void, 16)))
+    else:
+        vals = np.arange(n).astype({1: np.uint8, 2: np.uint16, 4: np.uint32,
+                                    8: np.uint64}[width])
+    gk, gv = _sort_pairs(launch, keys, vals, descending)
+    wk, wv = oracle.radix_sort(kind, keys, vals, descending=descending)
+    assert np.array_equal(_bits(gk), _bits(wk))
+    assert np.array_equal(gv.view(np.uint8), wv.view(np.uint8))
+
+
 def test_pairs_u64_keys_u32_values(launch):
     keys, values = workloads.c2_uniform(1 << 18)
     gk, gv = _sort_pairs(launch, keys, values)
