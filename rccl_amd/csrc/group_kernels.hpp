@@ -307,16 +307,13 @@ Layout layout(size_t n) {
   constexpr size_t TILE = tile_items<K, P, V>();
   l.tiles = (n + TILE - 1) / TILE;
   l.groups = (l.tiles + lookback::GROUP - 1) / lookback::GROUP;
-  size_t off = 0;
-  l.desc = off;  // descriptors, group words and the ticket are contiguous
-  off += l.tiles * sizeof(uint64_t);
-  l.gagg = off;
-  off += l.groups * sizeof(uint64_t);
-  l.ginc = off;
-  off += l.groups * sizeof(uint64_t);
-  l.ticket = off;
-  off += sizeof(uint64_t);
-  l.total = align_up(off, 256);
+  // Descriptors, group words and the ticket: one span (lookback::state_layout).
+  const lookback::State st = lookback::state_layout(l.tiles);
+  l.desc = 0;
+  l.gagg = st.gagg * sizeof(uint64_t);
+  l.ginc = st.ginc * sizeof(uint64_t);
+  l.ticket = st.ticket * sizeof(uint64_t);
+  l.total = align_up(st.words * sizeof(uint64_t), 256);
   return l;
 }
 

@@ -460,7 +460,20 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
 #pragma unroll
   for (int s = 0; s < SUB; ++s) total += sub[s].count;
 
-  // Two-level decoupled look-back for the block's output offset (wave 0).
+  auto compact = [&](const SubTile<K, VS, ITEMS, PAIRS> &r) {
+    uint32_t o = r.excl;
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+      if (r.mask & (1u << k)) {
+        sm.keys[o] = r.outk[k];
+        if constexpr (PAIRS) sm.vals[o] = r.outv[k];
+        ++o;
+      }
+    }
+  };
+  // Two-level decoupled look-back for the block's output offset (wave 0),
+  // while the other waves compact the first sub-tile into LDS (every read of
+  // the staged inputs lies before the last scan barrier).
   if (wave == 0) {
     const uint64_t prefix = lookback::tile_prefix(t, lb_tiles, total, desc, gagg, ginc, lane);
     if (lane == 0) {
@@ -468,31 +481,25 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
       sm.tile_offset = prefix;
     }
   }
+  if (out != nullptr) compact(sub[0]);
   lds_barrier();
   if (out == nullptr) return;  // count only
 
-  // Compact through LDS, then coalesced stores, one sub-tile at a time;
-  // positions at or past the destination's capacity are counted but not
-  // written.
+  // Coalesced stores from the LDS-compacted outputs, one sub-tile at a time
+  // (each later sub-tile compacted once the previous stores have read the
+  // buffer); positions at or past the destination's capacity are counted but
+  // not written.
   size_t base = sm.tile_offset;
 #pragma unroll
   for (int s = 0; s < SUB; ++s) {
     const SubTile<K, VS, ITEMS, PAIRS> &r = sub[s];
     if (base >= out_cap) return;  // uniform: the rest lies past the end
     const uint32_t keep = static_cast<uint32_t>(std::min<size_t>(r.count, out_cap - base));
-    if (s > 0) lds_barrier();  // the previous sub-tile's stores have read the buffer
-    {
-      uint32_t o = r.excl;
-#pragma unroll
-      for (int k = 0; k < ITEMS; ++k) {
-        if (r.mask & (1u << k)) {
-          sm.keys[o] = r.outk[k];
-          if constexpr (PAIRS) sm.vals[o] = r.outv[k];
-          ++o;
-        }
-      }
+    if (s > 0) {
+      lds_barrier();  // the previous sub-tile's stores have read the buffer
+      compact(r);
+      lds_barrier();
     }
-    lds_barrier();
     constexpr int STORE = (Smem::CAP + THREADS - 1) / THREADS;
 #pragma unroll
     for (int k = 0; k < STORE; ++k) {
@@ -551,14 +558,13 @@ Layout layout(size_t na, size_t nb) {
   size_t off = 0;
   l.splits = off;
   off += align_up((l.tiles + 1) * 2 * sizeof(uint64_t), 256);
+  // Descriptors, group words and the ticket: one span (lookback::state_layout).
+  const lookback::State st = lookback::state_layout(l.lb_tiles);
   l.desc = off;
-  off += l.lb_tiles * sizeof(uint64_t);
-  l.gagg = off;
-  off += l.groups * sizeof(uint64_t);
-  l.ginc = off;
-  off += l.groups * sizeof(uint64_t);
-  l.ticket = off;
-  off += sizeof(uint64_t);
+  l.gagg = off + st.gagg * sizeof(uint64_t);
+  l.ginc = off + st.ginc * sizeof(uint64_t);
+  l.ticket = off + st.ticket * sizeof(uint64_t);
+  off += st.words * sizeof(uint64_t);
   l.sampled = ordering::sampled_partition_for<K>() && na > 0 && nb > 0 &&
               l.tiles >= SAMPLED_MIN_TILES;
   if (l.sampled) {

@@ -465,15 +465,16 @@ def test_sampled_partition_workspaces(lib):
     setop = lambda na, nb, key: _abi.workspace_bytes(
         "rccl_hip_set_op_workspace_bytes", 0, key, 0, na, nb)
     # u32 keys only: 8,192-item partition tiles, two per look-back tile,
-    # groups of 64 look-back tiles. 2^21 items = 256 tiles: splits
-    # 257 * 16 B -> 4,352 B, then 128 descriptors, 2 + 2 group words and the
-    # ticket (1,064 B) -> 5,632 B.
-    assert setop(1 << 20, 1 << 20, 0) == 5632
-    # 2^23 items = 1,024 tiles: splits 1,025 * 16 B -> 16,640 B, 512
-    # descriptors, 8 + 8 group words, the ticket -> 20,872 B, aligned to
-    # 20,992 B, plus 2,048 sample counts -> 29,184 B; f32 keys: 20,992 B.
-    assert setop(1 << 22, 1 << 22, 0) == 29184
-    assert setop(1 << 22, 1 << 22, 2) == 20992
+    # groups of 64 look-back tiles; the look-back state is the descriptors,
+    # a 16-word gap, the group aggregates, another 16-word gap, the group
+    # prefixes and the ticket. 2^21 items = 256 tiles: splits 257 * 16 B ->
+    # 4,352 B, then 128 + 16 + 2 + 16 + 2 + 1 words (1,320 B) -> 5,888 B.
+    assert setop(1 << 20, 1 << 20, 0) == 5888
+    # 2^23 items = 1,024 tiles: splits 1,025 * 16 B -> 16,640 B, then
+    # 512 + 16 + 8 + 16 + 8 + 1 words (4,488 B) -> 21,128 B, aligned to
+    # 21,248 B, plus 2,048 sample counts -> 29,440 B; f32 keys: 21,248 B.
+    assert setop(1 << 22, 1 << 22, 0) == 29440
+    assert setop(1 << 22, 1 << 22, 2) == 21248
 
 
 def test_radix_wide_descriptors_from_2pow30(lib):
