@@ -278,7 +278,9 @@ RCCL_HIP_API rccl_hip_status rccl_hip_merge_sort_workspace_bytes(rccl_hip_key_ki
                                                     size_t *bytes);
 
 /* Stable merge sort. in_keys == out_keys (and in_values == out_values) sorts
- * in place; otherwise the inputs are left untouched (the _copy forms).
+ * in place; otherwise the inputs are left untouched (the _copy forms). Float
+ * keys compare with IEEE `<` (-0.0 and +0.0 are equal and keep their input
+ * order); inputs holding NaN, which `<` cannot order, have no defined order.
  * Replaces device_merge_sort_{keys,pairs}{,_copy}
  * (rccl-cub/src/dispatch.rs:170-322,1116-1400; rccl-cub/src/merge_sort.rs:156-690)
  * and Thrust sort_by / sort_unstable_by (rccl-thrust/src/backend.rs:39-150). */

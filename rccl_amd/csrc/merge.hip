@@ -54,19 +54,22 @@ rccl_hip_status merge_run(rccl_hip_key_kind key, const merge::MergeArgs &m, size
   return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "merge key kind");
 }
 
-// Merge sorts of at least this many items with 32- or 64-bit integer keys run
-// as a stable LSD radix sort (radix::merge_sort_lowering): same permutation,
-// 36 B/key of HBM traffic for u32 keys instead of 8 B per merge level. Float
-// keys stay on the merge sort, whose comparisons treat -0.0 and +0.0 as equal
-// and order NaN unlike their bits.
+// Merge sorts of at least this many items with 32- or 64-bit keys run as a
+// stable LSD radix sort (radix::merge_sort_lowering): same permutation, 36
+// B/key of HBM traffic for 4-byte keys instead of 8 B per merge level. That
+// holds for float keys too: the radix order is IEEE order with -0.0 and +0.0
+// one key, which is the merge sort's `<`. Only NaN differs, and with NaN `<`
+// is no ordering at all (a partial_cmp comparator cannot take it), so such
+// inputs have no defined order either way.
 #ifndef RCCL_MERGE_SORT_RADIX_MIN_ITEMS
 #define RCCL_MERGE_SORT_RADIX_MIN_ITEMS 65536
 #endif
 
 bool lowers_to_radix(rccl_hip_key_kind key, size_t n) {
-  const bool integer = key == RCCL_HIP_KEY_U32 || key == RCCL_HIP_KEY_I32 ||
-                       key == RCCL_HIP_KEY_U64 || key == RCCL_HIP_KEY_I64;
-  return integer && n >= RCCL_MERGE_SORT_RADIX_MIN_ITEMS && n <= radix::MAX_ITEMS;
+  const bool wide = key == RCCL_HIP_KEY_U32 || key == RCCL_HIP_KEY_I32 ||
+                    key == RCCL_HIP_KEY_F32 || key == RCCL_HIP_KEY_U64 ||
+                    key == RCCL_HIP_KEY_I64 || key == RCCL_HIP_KEY_F64;
+  return wide && n >= RCCL_MERGE_SORT_RADIX_MIN_ITEMS && n <= radix::MAX_ITEMS;
 }
 
 size_t merge_sort_bytes(rccl_hip_key_kind key, size_t n, size_t vb) {

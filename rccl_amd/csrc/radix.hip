@@ -254,9 +254,11 @@ size_t merge_sort_lowering_bytes(size_t key_bytes_, size_t value_bytes, size_t n
          layout(key_bytes_, value_bytes, n).total + plan_bytes();
 }
 
-// A stable LSD radix sort of integer keys under the natural order or its
-// reverse yields exactly the stable merge sort's permutation: digit order is
-// integer order, and equal keys keep their input order. The output buffers
+// A stable LSD radix sort under the natural order or its reverse yields
+// exactly the stable merge sort's permutation: digit order is integer order,
+// or for floats IEEE order with -0.0 and +0.0 one key (the merge sort's `<`;
+// inputs with NaN, which `<` cannot order, have no defined order), and equal
+// keys keep their input order. The output buffers
 // are the first half of the double buffer and the workspace's scratch the
 // second; a copy form reads its input in the histogram and its first active
 // pass only. The sort is planned: passes whose byte is the same in every key
@@ -267,8 +269,8 @@ rccl_hip_status merge_sort_lowering(rccl_hip_key_kind key, size_t value_bytes, b
                                     void *out_vals, size_t n, void *workspace,
                                     size_t workspace_bytes, hipStream_t stream) {
   const size_t kb = key_bytes(key);
-  if (key != RCCL_HIP_KEY_U32 && key != RCCL_HIP_KEY_I32 && key != RCCL_HIP_KEY_U64 &&
-      key != RCCL_HIP_KEY_I64)
+  if (key != RCCL_HIP_KEY_U32 && key != RCCL_HIP_KEY_I32 && key != RCCL_HIP_KEY_F32 &&
+      key != RCCL_HIP_KEY_U64 && key != RCCL_HIP_KEY_I64 && key != RCCL_HIP_KEY_F64)
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "merge sort radix key kind");
   const size_t scratch = align_up(n * kb, 256) + align_up(n * value_bytes, 256);
   if (!workspace || workspace_bytes < merge_sort_lowering_bytes(kb, value_bytes, n))

@@ -312,6 +312,38 @@ def test_merge_sort_radix_lowering(launch, radix_ranking, kind):
                     assert v.to_host_vec().tobytes() == vals.tobytes(), "input modified"
 
 
+@pytest.mark.parametrize("kind", ["f32", "f64"])
+def test_merge_sort_float_radix_lowering_signed_zeros(launch, radix_ranking, kind):
+    """Float keys from 65,536 items also sort through the radix lowering. The
+    merge sort's order is IEEE `<`, under which -0.0 and +0.0 are equal: they
+    must keep their input order, as the oracle's comparison merge sort keeps
+    them. A quarter of the keys are signed zeros, interleaved; the rest are
+    small signed values with ties, and +-inf and denormals. Payloads record
+    the input order."""
+    dt = np.dtype(DTYPES[kind])
+    for idx, n in enumerate([65_535, 65_536, 300_007]):
+        raw = workloads.hash_range(1300 + idx, n)
+        keys = ((raw % np.uint64(41)).astype(np.int64) - 20).astype(dt)
+        sel = raw >> np.uint64(58)  # 0..63
+        keys[sel < 8] = dt.type(0.0)
+        keys[(sel >= 8) & (sel < 16)] = dt.type(-0.0)
+        keys[sel == 16] = dt.type(np.inf)
+        keys[sel == 17] = dt.type(-np.inf)
+        keys[sel == 18] = np.finfo(dt).smallest_subnormal
+        keys[sel == 19] = -np.finfo(dt).smallest_subnormal
+        vals = np.arange(n, dtype=np.uint32)
+        for descending in (False, True):
+            wk, wv = oracle.merge_sort(kind, keys, vals, descending)
+            for copy in (False, True):
+                gk, gv = _merge_sort(launch, keys, vals, descending, copy=copy)
+                assert np.array_equal(_bits(gk), _bits(wk)), (kind, n, descending, copy)
+                assert np.array_equal(gv, wv), (kind, n, descending, copy)
+            zeros = (_bits(wk) << np.uint64(1) if dt.itemsize == 8 else
+                     _bits(wk) << np.uint32(1)) == 0
+            assert np.signbit(wk[zeros]).any() and not np.signbit(wk[zeros]).all()
+            assert np.all(np.diff(wv[zeros].astype(np.int64)) > 0)  # input order
+
+
 def test_merge_sort_c4_full_size(launch, radix_ranking):
     """The benchmark's C4 merge sort (2^26 u32 keys in [0, 2^24), copy form),
     bit-exact with numpy's stable sort (keys only, so any correct sort is the
