@@ -129,7 +129,7 @@ template <class Desc> struct LookbackBuf {
 #define RCCL_RADIX_PAIRS_ITEMS_4B 28
 #endif
 #ifndef RCCL_RADIX_PAIRS_ITEMS_8B
-#define RCCL_RADIX_PAIRS_ITEMS_8B 14
+#define RCCL_RADIX_PAIRS_ITEMS_8B 16
 #endif
 #ifndef RCCL_RADIX_PAIRS_ITEMS_16B
 #define RCCL_RADIX_PAIRS_ITEMS_16B 7
