@@ -132,7 +132,7 @@ template <class Desc> struct LookbackBuf {
 #define RCCL_RADIX_PAIRS_ITEMS_8B 16
 #endif
 #ifndef RCCL_RADIX_PAIRS_ITEMS_16B
-#define RCCL_RADIX_PAIRS_ITEMS_16B 7
+#define RCCL_RADIX_PAIRS_ITEMS_16B 8
 #endif
 #ifndef RCCL_RADIX_LOOKBACK_WINDOW
 #define RCCL_RADIX_LOOKBACK_WINDOW 16
