@@ -45,10 +45,12 @@ rccl_hip_status static_workspace(void **out) {
   return ok();
 }
 
-Layout layout(size_t key_bytes, size_t value_bytes, size_t n) {
+Layout layout(size_t key_bytes, size_t value_bytes, size_t n, bool planned) {
   Layout l;
   const size_t max_passes = key_bytes;  // 8-bit digits
-  const size_t tile = tile_items(key_bytes, value_bytes);
+  l.small = small_tiles(key_bytes, value_bytes, n, planned);
+  const size_t tile =
+      l.small ? small_tile_items(key_bytes, value_bytes) : tile_items(key_bytes, value_bytes);
   l.tiles = (n + tile - 1) / tile;
   l.desc_bytes = n < (size_t(1) << 30) ? 4 : 8;
   size_t off = 0;
@@ -230,7 +232,7 @@ rccl_hip_status sort_buffer(rccl_hip_key_kind key, size_t value_bytes, rccl_hip_
   if (!a.keys[0] || !a.keys[1]) return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix keys");
   if (value_bytes && (!a.vals[0] || !a.vals[1]))
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix values");
-  const Layout l = layout(key_bytes(key), value_bytes, a.n);
+  const Layout l = layout(key_bytes(key), value_bytes, a.n, a.planned);
   if (!a.ws || workspace_bytes < l.total)
     return set_error(RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL, "radix workspace", l.total,
                      workspace_bytes);
@@ -251,7 +253,7 @@ rccl_hip_status sort_buffer(rccl_hip_key_kind key, size_t value_bytes, rccl_hip_
 
 size_t merge_sort_lowering_bytes(size_t key_bytes_, size_t value_bytes, size_t n) {
   return align_up(n * key_bytes_, 256) + align_up(n * value_bytes, 256) +
-         layout(key_bytes_, value_bytes, n).total + plan_bytes();
+         layout(key_bytes_, value_bytes, n, true).total + plan_bytes();
 }
 
 // A stable LSD radix sort under the natural order or its reverse yields
@@ -328,7 +330,7 @@ rccl_hip_status rccl_hip_radix_sort_workspace_bytes(rccl_hip_key_kind key, size_
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix value bytes");
   if (n > radix::MAX_ITEMS)
     return set_error(RCCL_HIP_ERROR_LENGTH_MISMATCH, "radix item count", radix::MAX_ITEMS, n);
-  *bytes = radix::layout(key_bytes(key), value_bytes, n).total;
+  *bytes = radix::layout(key_bytes(key), value_bytes, n, false).total;
   return ok();
 }
 
@@ -368,7 +370,7 @@ rccl_hip_status rccl_hip_radix_sort_static(rccl_hip_key_kind key, size_t value_b
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix value bytes");
   if (n > radix::MAX_ITEMS)
     return set_error(RCCL_HIP_ERROR_LENGTH_MISMATCH, "radix item count", radix::MAX_ITEMS, n);
-  const size_t need = radix::layout(key_bytes(key), value_bytes, n).total;
+  const size_t need = radix::layout(key_bytes(key), value_bytes, n, false).total;
   if (need > RCCL_HIP_STATIC_RADIX_WORKSPACE_BYTES)
     return set_error(RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL, "static radix workspace", need,
                      RCCL_HIP_STATIC_RADIX_WORKSPACE_BYTES);

@@ -184,6 +184,33 @@ constexpr size_t tile_items(size_t key_bytes, size_t value_bytes) {
   return size_t(threads_for(value_bytes)) * items_for(key_bytes, value_bytes);
 }
 
+// Small-input tiles: inputs of at most RCCL_RADIX_SMALL_MAX_TILES small tiles
+// use blocks of SMALL_THREADS threads with half the items, a quarter of a keys
+// tile (an eighth of a pairs tile), so that a cache-resident input still
+// spreads over every CU: 2^20 u32 keys make 241 tiles instead of 61 (76 -> 66
+// us per sort). Measured crossover: small tiles are faster up to 2^21 u32 keys
+// and 2^20 u64 + u32 pairs (512 small tiles), slower from 2^22 and 2^21.
+// Sorts with a pass plan (the merge-sort lowering) keep the large tiles.
+#ifndef RCCL_RADIX_SMALL_THREADS
+#define RCCL_RADIX_SMALL_THREADS 256
+#endif
+#ifndef RCCL_RADIX_SMALL_MAX_TILES
+#define RCCL_RADIX_SMALL_MAX_TILES 512
+#endif
+constexpr int SMALL_THREADS = RCCL_RADIX_SMALL_THREADS;
+constexpr int small_items_for(size_t key_bytes, size_t value_bytes) {
+  return items_for(key_bytes, value_bytes) / 2 > 0 ? items_for(key_bytes, value_bytes) / 2 : 1;
+}
+constexpr size_t small_tile_items(size_t key_bytes, size_t value_bytes) {
+  return size_t(SMALL_THREADS) * small_items_for(key_bytes, value_bytes);
+}
+// Whether a sort of n items uses the small tiles (the layout and the launches
+// both ask this).
+constexpr bool small_tiles(size_t key_bytes, size_t value_bytes, size_t n, bool planned) {
+  return !planned && n <= size_t(RCCL_RADIX_SMALL_MAX_TILES) * small_tile_items(key_bytes,
+                                                                               value_bytes);
+}
+
 // ---------------------------------------------------------------------------
 // init: zero the bins. (Internal linkage: every translation unit that
 // launches it carries its own copy.)
@@ -289,6 +316,7 @@ histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__
   }
 }
 
+
 // Pass plan of a sort that skips trivial passes (one digit holds every key:
 // the pass would not move anything). Buffers: 0 the input, 1 the output,
 // 2 the scratch; lb is the look-back buffer of the pass (the active passes
@@ -344,7 +372,10 @@ __device__ inline void assign_plan(int P, uint32_t trivial, uint32_t flags,
 // position of each digit), once, so the onesweep blocks read them instead of
 // each scanning the bins. One block of BINS threads. With a plan, it also
 // marks the trivial passes (a digit counting all n keys) and writes the pass
-// plan. (Internal linkage, like init_kernel.)
+// plan. A separate launch: folding it into the histogram's last block (a
+// device-scope completion counter) measured slower at 2^28 (229 against 216
+// us), as the agent-scope release writes back every block's dirty L2 lines.
+// (Internal linkage, like init_kernel.)
 namespace {
 __global__ void __launch_bounds__(BINS)
 bins_scan_kernel(uint32_t *bins, uint32_t passes, uint32_t n, PassPlan *plan,
@@ -1006,6 +1037,7 @@ struct Layout {
   size_t tiles = 0;
   size_t groups = 0;
   size_t desc_bytes = 4;
+  bool small = false;  // small_tiles()
   size_t bins = 0;
   // Look-back buffers: tile descriptors, group prefixes, group aggregates and
   // the pass's tile tickets.
@@ -1014,7 +1046,7 @@ struct Layout {
   size_t total = 0;
 };
 
-Layout layout(size_t key_bytes, size_t value_bytes, size_t n);
+Layout layout(size_t key_bytes, size_t value_bytes, size_t n, bool planned);
 
 // Per-device facts a onesweep launch needs, found once per device
 // (radix.hip): whether the LDS serves same-address atomic lanes in lane
@@ -1068,29 +1100,29 @@ void lookback_buffers(const SortArgs &a, const Layout &l, LookbackBuf<Desc> (&lb
   }
 }
 
-// The onesweep launches of a sort, in one ranking mode.
-template <class Bits, class Val, class Ops, class Desc, Rank RANK>
+// The onesweep launches of a sort, in one ranking mode and tile shape, with
+// or without a pass plan.
+template <class Bits, class Val, class Ops, class Desc, Rank RANK, int THREADS, int ITEMS,
+          bool PLANNED>
 rccl_hip_status launch_onesweeps(SortArgs &a, const Layout &l, uint32_t passes,
                                  const uint32_t *bins, const PassPlan *plan, uint32_t nx) {
-  constexpr size_t VBYTES = std::is_same<Val, NoValue>::value ? 0 : sizeof(Val);
-  constexpr int ITEMS = items_for(sizeof(Bits), VBYTES);
-  constexpr int THREADS = threads_for(VBYTES);
   LookbackBuf<Desc> lb[2];
   lookback_buffers(a, l, lb);
   size_t resident = 0;
-  RCCL_HIP_TRY(resident_blocks(
-      a.planned
-          ? reinterpret_cast<const void *>(
-                &planned_onesweep_kernel<Bits, Val, Ops, ITEMS, Desc, THREADS, RANK>)
-          : reinterpret_cast<const void *>(
-                &onesweep_kernel<Bits, Val, Ops, ITEMS, Desc, THREADS, RANK>),
-      THREADS, &resident));
+  const void *kernel;
+  if constexpr (PLANNED)
+    kernel = reinterpret_cast<const void *>(
+        &planned_onesweep_kernel<Bits, Val, Ops, ITEMS, Desc, THREADS, RANK>);
+  else
+    kernel = reinterpret_cast<const void *>(
+        &onesweep_kernel<Bits, Val, Ops, ITEMS, Desc, THREADS, RANK>);
+  RCCL_HIP_TRY(resident_blocks(kernel, THREADS, &resident));
   // The XCD order needs two rows of runs resident at once; with fewer, blocks
   // claim ticketed tiles instead.
   if (nx == XCDS && resident < 2 * size_t(XCDS) * XCD_RUN) nx = 1;
   const uint32_t grid = static_cast<uint32_t>(onesweep_grid(l.tiles, nx));
 
-  if (a.planned) {
+  if constexpr (PLANNED) {
     const PlanBuffers<Bits, Val> b{
         static_cast<const Bits *>(a.src_keys ? a.src_keys : a.keys[0]),
         static_cast<Bits *>(a.keys[0]), static_cast<Bits *>(a.keys[1]),
@@ -1173,6 +1205,7 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
       err = hipDeviceGetAttribute(&hist_cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "radix device", err);
   }
+  PassPlan *plan = a.planned ? reinterpret_cast<PassPlan *>(a.ws + l.total) : nullptr;
   {
     KernelTimer t("radix_histogram", a.stream, a.n);
     const size_t chunk = size_t(HIST_THREADS) * HIST_ITEMS;
@@ -1187,18 +1220,36 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
         zero_words);
   }
   RCCL_HIP_TRY(check_launch("radix histogram"));
-  PassPlan *plan = a.planned ? reinterpret_cast<PassPlan *>(a.ws + l.total) : nullptr;
   {
     KernelTimer t("radix_bins_scan", a.stream, passes * BINS);
     bins_scan_kernel<<<1, BINS, 0, a.stream>>>(bins, passes, static_cast<uint32_t>(a.n), plan,
                                                 a.plan_flags);
   }
   RCCL_HIP_TRY(check_launch("radix bins scan"));
-  return caps.rank == Rank::LaneAtomic
-             ? launch_onesweeps<Bits, Val, Ops, Desc, Rank::LaneAtomic>(a, l, passes, bins, plan,
-                                                                        caps.nx)
-             : launch_onesweeps<Bits, Val, Ops, Desc, Rank::MatchAny>(a, l, passes, bins, plan,
-                                                                      caps.nx);
+  constexpr int ITEMS = items_for(sizeof(Bits), VBYTES);
+  constexpr int THREADS = threads_for(VBYTES);
+  constexpr int SITEMS = small_items_for(sizeof(Bits), VBYTES);
+  constexpr Rank LA = Rank::LaneAtomic, MA = Rank::MatchAny;
+  const bool la = caps.rank == LA;
+  if (a.planned)
+    return la ? launch_onesweeps<Bits, Val, Ops, Desc, LA, THREADS, ITEMS, true>(
+                    a, l, passes, bins, plan, caps.nx)
+              : launch_onesweeps<Bits, Val, Ops, Desc, MA, THREADS, ITEMS, true>(
+                    a, l, passes, bins, plan, caps.nx);
+  // Small tiles serve unplanned sorts only, all below 2^30 items (32-bit
+  // descriptors); the layout chose them for this n.
+  if constexpr (sizeof(Desc) == 4) {
+    if (l.small)
+      return la ? launch_onesweeps<Bits, Val, Ops, Desc, LA, SMALL_THREADS, SITEMS, false>(
+                      a, l, passes, bins, plan, caps.nx)
+                : launch_onesweeps<Bits, Val, Ops, Desc, MA, SMALL_THREADS, SITEMS, false>(
+                      a, l, passes, bins, plan, caps.nx);
+  }
+  if (l.small) return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix small-tile layout");
+  return la ? launch_onesweeps<Bits, Val, Ops, Desc, LA, THREADS, ITEMS, false>(
+                  a, l, passes, bins, plan, caps.nx)
+            : launch_onesweeps<Bits, Val, Ops, Desc, MA, THREADS, ITEMS, false>(
+                  a, l, passes, bins, plan, caps.nx);
 }
 
 template <class Bits, class Ops>

@@ -11,6 +11,8 @@ import sys
 import numpy as np
 import pytest
 
+import radix_shapes
+
 from rccl_amd import _abi, cub, workloads
 from rccl_amd.device import KIND_DTYPES, kind_of
 
@@ -256,10 +258,16 @@ def test_merge_sort_radix_lowering_workspace(lib, key, kb, vb):
     state; below the threshold and for float keys it is the merge sort's."""
     def align(x):
         return (x + 255) // 256 * 256
-    for n in (65_536, 1 << 22):
+    for n in (65_536, 1 << 23):
         ms = _abi.workspace_bytes("rccl_hip_merge_sort_workspace_bytes", key, vb, n)
         radix = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", key, vb, n)
-        assert ms >= align(n * kb) + align(n * vb) + radix
+        # The lowering keeps the large tiles; a plain radix sort of up to 512
+        # small tiles (below 2^22 items for every key and value width) uses
+        # small ones, whose control state is larger.
+        if n >= 1 << 23:
+            assert ms >= align(n * kb) + align(n * vb) + radix
+        else:
+            assert ms > align(n * kb) + align(n * vb)
         # Below the threshold: the merge sort's own workspace, no radix state.
         assert _abi.workspace_bytes("rccl_hip_merge_sort_workspace_bytes", key, vb, 65_535) < \
             align(65_535 * kb) + align(65_535 * vb) + radix
@@ -267,6 +275,20 @@ def test_merge_sort_radix_lowering_workspace(lib, key, kb, vb):
     need = _abi.workspace_bytes("rccl_hip_merge_sort_workspace_bytes", key, vb, 70_000)
     assert lib.rccl_hip_merge_sort(key, vb, 0, FAKE, FAKE if vb else None, FAKE,
                                    FAKE if vb else None, 70_000, FAKE, need - 1, None) == 2
+
+
+@pytest.mark.parametrize("key,kb", [(0, 4), (3, 8)])
+@pytest.mark.parametrize("vb", [0, 1, 2, 4, 8, 16])
+def test_radix_small_tile_threshold(key, kb, vb):
+    """Plain sorts of at most 512 small tiles (256 threads x half a large
+    tile's items) use them; one item more takes the large tiles, whose
+    control state is about a quarter as large (an eighth for pairs)."""
+    m = radix_shapes.small_tile_max(kb, vb)
+    at = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", key, vb, m)
+    below = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", key, vb, m - 1)
+    above = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", key, vb, m + 1)
+    assert at == below
+    assert above * 3 < at
 
 
 def test_python_mirror_host_logic():

@@ -5,10 +5,13 @@ Cases follow the reference's own probes
 device_radix_sort_pairs_probe.rs); every output is compared bit-for-bit with
 the CPU oracle (oracle/oracle.c) on the same input.
 """
+import functools
+
 import numpy as np
 import pytest
 
 import oracle
+import radix_shapes
 from rccl_amd import cub, workloads
 from rccl_amd.device import DeviceBuffer
 
@@ -369,3 +372,42 @@ def test_single_tile_windows_flip_once(launch, window):
     np.testing.assert_array_equal(ck.to_host_vec(), wk)
     np.testing.assert_array_equal(cv.to_host_vec(), wv)
     np.testing.assert_array_equal(k0.to_host_vec(), host)  # the input is left as it was
+
+
+# Both tile shapes: plain sorts of at most 512 small tiles use 256-thread
+# blocks with half the items; one item more takes the large tiles. Inputs and
+# oracle outputs are shared by the ranking modes.
+@functools.lru_cache(maxsize=4)
+def _threshold_case(kind, width, n, descending):
+    dt = np.dtype(oracle.KIND_DTYPES[kind])
+    raw = workloads.hash_range(0x51A11 + 131 * dt.itemsize + width, n)
+    keys = ((raw >> np.uint64(32)).astype(np.uint32) if dt.itemsize == 4 else raw).view(dt)
+    keys = keys.copy()
+    if dt.kind == "f":
+        _bits(keys)[::97] = 0
+        _bits(keys)[1::89] = 1 << (dt.itemsize * 8 - 1)
+    if width == 0:
+        return keys, None, oracle.radix_sort(kind, keys, descending=descending), None
+    if width == 16:
+        values = workloads.hash_range(0xBEEF, 2 * n).view(np.dtype("V16"))
+    else:
+        values = np.arange(n, dtype=np.uint64).astype(np.dtype(f"u{width}"))
+    wk, wv = oracle.radix_sort(kind, keys, values, descending=descending)
+    return keys, values, wk, wv
+
+
+@pytest.mark.parametrize("side", ["small_max", "large_min"])
+@pytest.mark.parametrize("kind,width", [(k, 0) for k in ("u32", "i32", "f32", "u64", "i64", "f64")]
+                         + [("u32", w) for w in (1, 2, 4, 8, 16)] + [("u64", 4), ("u64", 16)])
+@pytest.mark.parametrize("descending", [False, True])
+def test_tile_shape_threshold(launch, kind, width, side, descending):
+    dt = np.dtype(oracle.KIND_DTYPES[kind])
+    n = radix_shapes.small_tile_max(dt.itemsize, width) + (side == "large_min")
+    keys, values, wk, wv = _threshold_case(kind, width, n, descending)
+    if values is None:
+        got = _sort_keys(launch, keys, descending)
+        np.testing.assert_array_equal(_bits(got), _bits(wk))
+    else:
+        gk, gv = _sort_pairs(launch, keys, values, descending)
+        np.testing.assert_array_equal(_bits(gk), _bits(wk))
+        assert np.array_equal(gv, wv)
