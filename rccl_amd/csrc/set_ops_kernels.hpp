@@ -311,8 +311,11 @@ struct SubTile {
 // back once for all of them, and stores them in turn. SUB = 2 halves the
 // look-backs at the same LDS footprint (two blocks per CU).
 // Two blocks per CU (4 waves per SIMD): a register budget of 128.
+#ifndef RCCL_SET_WAVES_PER_SIMD
+#define RCCL_SET_WAVES_PER_SIMD 4
+#endif
 template <class K, class V, class Cmp, int OP, int ITEMS, int SUB, bool ARITH>
-__global__ void __launch_bounds__(THREADS, 4)
+__global__ void __launch_bounds__(THREADS, RCCL_SET_WAVES_PER_SIMD)
 tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restrict__ b,
             const V *__restrict__ bv, const uint64_t *__restrict__ splits, size_t tiles,
             size_t lb_tiles, K *__restrict__ out, V *__restrict__ outv, size_t out_cap,
