@@ -113,46 +113,143 @@ __device__ __forceinline__ size_t first_not_before(const K *__restrict__ arr, si
   return a;
 }
 
-// Items searched a whole line at a time: 4 to 16 bytes that tile 128 bytes
-// (narrower ones would need a register per item to compare).
+// Items searched a whole line at a time: 4, 8 or 16 bytes, a whole number
+// per 16-byte lane read (narrower ones would need a register per item).
 template <class K>
 constexpr bool line_items() {
-  return sizeof(K) >= 4 && 128 % sizeof(K) == 0;
+  return sizeof(K) >= 4 && 16 % sizeof(K) == 0;
 }
 
-// Number of the first `valid` items of a 16-byte-aligned 128-byte line that
-// are before x: the line is read whole with eight independent 16-byte loads
-// and compared in registers, one memory round trip where a binary search
-// inside the line chains five.
+// Shuffle of a trivially copyable item, one 32-bit word at a time.
+template <class T>
+__device__ __forceinline__ T shfl_item(const T &v, int src) {
+  static_assert(sizeof(T) % 4 == 0, "whole words");
+  uint32_t w[sizeof(T) / 4];
+  __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+  for (size_t i = 0; i < sizeof(T) / 4; ++i)
+    w[i] = static_cast<uint32_t>(__shfl(static_cast<int>(w[i]), src, 64));
+  T r;
+  __builtin_memcpy(&r, w, sizeof(T));
+  return r;
+}
+
+// For every lane of the (fully active) wave: how many of the first `valid`
+// items of the 128-byte line at base + start are before the lane's x. Eight
+// lanes read each line together, 16 bytes a lane, and add their counts with
+// three butterfly shuffles; eight rounds cover the wave's 64 lines, all eight
+// loads issued before the first is used. A load instruction so touches eight
+// lines (one per needle) instead of 64: lane-private reads of whole lines
+// (eight 16-byte loads per lane per line) were bound by the address
+// processing of 64 lines per instruction. `base` is 16-byte aligned and
+// every line lies inside its array (a lane with nothing to search passes
+// start 0 and valid 0).
 template <class K, class B>
-__device__ __forceinline__ uint32_t count_before(const K *__restrict__ line, uint32_t valid,
-                                                 const K &x, B before) {
-  static_assert(128 % sizeof(K) == 0, "whole items per line");
-  constexpr int ITEMS = 128 / sizeof(K);
+__device__ __forceinline__ uint32_t group_count_before(const K *__restrict__ base, size_t start,
+                                                       uint32_t valid, const K &x, B before,
+                                                       uint32_t lane) {
+  static_assert(16 % sizeof(K) == 0, "whole items per 16 bytes");
+  constexpr int PER = 16 / sizeof(K);
+  const uint32_t sub = lane & 7u, grp = lane >> 3;
   uint4 raw[8];
-  const uint4 *p = reinterpret_cast<const uint4 *>(line);
+  uint32_t vld[8];
+  K xr[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) raw[i] = p[i];
-  K v[ITEMS];
-  __builtin_memcpy(v, raw, 128);
-  uint32_t cnt = 0;
+  for (int r = 0; r < 8; ++r) {
+    const int src = r * 8 + static_cast<int>(grp);
+    const size_t st = shfl_item(start, src);
+    vld[r] = static_cast<uint32_t>(__shfl(static_cast<int>(valid), src, 64));
+    xr[r] = shfl_item(x, src);
+    raw[r] = reinterpret_cast<const uint4 *>(base + st)[sub];
+  }
+  uint32_t mine = 0;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) cnt += (uint32_t(i) < valid && before(v[i], x)) ? 1u : 0u;
-  return cnt;
+  for (int r = 0; r < 8; ++r) {
+    K v[PER];
+    __builtin_memcpy(v, &raw[r], 16);
+    uint32_t c = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      c += (sub * PER + uint32_t(i) < vld[r] && before(v[i], xr[r])) ? 1u : 0u;
+    c += static_cast<uint32_t>(__shfl_xor(static_cast<int>(c), 1, 64));
+    c += static_cast<uint32_t>(__shfl_xor(static_cast<int>(c), 2, 64));
+    c += static_cast<uint32_t>(__shfl_xor(static_cast<int>(c), 4, 64));
+    // Group g now holds the count of lane 8r + g's line; lane 8r + g takes
+    // it from the group's first lane.
+    const uint32_t got = static_cast<uint32_t>(__shfl(static_cast<int>(c), int((lane & 7u) << 3), 64));
+    if ((lane >> 3) == uint32_t(r)) mine = got;
+  }
+  return mine;
+}
+
+// Indexed search for items of 4, 8 or 16 bytes (all keys of 4 or 8 bytes,
+// rows of arity 2 and 4) whose `lines` array the LDS sample covers: the
+// sample (the last entry of every 128-byte line of `lines`) brackets the line
+// of `lines`, and each level below is one line read cooperatively
+// (group_count_before): the line of `lines` gives the index line, that gives
+// the haystack chunk, and the chunk the answer. A chunk that is not whole or
+// a haystack that is not 16-byte aligned is finished by binary search. The
+// needle loop is wave-uniform (the shuffles need every lane).
+template <class K, class Cmp, bool UPPER, uint32_t SAMPLES>
+__global__ void __launch_bounds__(THREADS)
+line_search_kernel(const K *__restrict__ hay, size_t n, const K *__restrict__ index,
+                   size_t chunks, const K *__restrict__ lines, size_t nlines,
+                   const K *__restrict__ needles, size_t m, uint64_t *__restrict__ out,
+                   bool hay16) {
+  __shared__ K sample[SAMPLES];
+  constexpr size_t CHUNK = chunk_items<K>();
+  const Before<K, Cmp, UPPER> before{};
+  const uint32_t used = static_cast<uint32_t>(std::min<size_t>(SAMPLES, nlines / CHUNK));
+  for (uint32_t s = threadIdx.x; s < used; s += THREADS)
+    sample[s] = lines[(size_t(s) + 1) * CHUNK - 1];
+  __syncthreads();
+  const uint32_t lane = threadIdx.x & 63u;
+  for (size_t b0 = size_t(blockIdx.x) * THREADS; b0 < m; b0 += size_t(gridDim.x) * THREADS) {
+    const size_t q = b0 + threadIdx.x;
+    const K x = needles[std::min(q, m - 1)];
+    // Line L of `lines`: the first whose last entry is not before x (L ==
+    // used is the partial last line, or past the end).
+    uint32_t lo = 0, hi = used;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) >> 1;
+      if (before(sample[mid], x)) lo = mid + 1;
+      else hi = mid;
+    }
+    const size_t l0 = size_t(lo) * CHUNK;
+    bool go = l0 < nlines;
+    const size_t j =
+        l0 + group_count_before(lines, go ? l0 : 0,
+                                go ? uint32_t(std::min(CHUNK, nlines - l0)) : 0u, x, before,
+                                lane);
+    go = go && j < nlines;
+    const size_t i0 = go ? j * CHUNK : 0;
+    // Below chunks for a sorted haystack; clamped so that an unsorted one
+    // (unspecified results) still reads in bounds.
+    const size_t c = std::min(
+        chunks - 1, i0 + group_count_before(index, i0,
+                                            go ? uint32_t(std::min(CHUNK, chunks - i0)) : 0u,
+                                            x, before, lane));
+    const size_t h0 = c * CHUNK;
+    const bool whole = go && h0 + CHUNK <= n;
+    size_t p = n;
+    if (hay16) {  // uniform
+      const uint32_t k = group_count_before(hay, whole ? h0 : 0, whole ? uint32_t(CHUNK) : 0u,
+                                            x, before, lane);
+      if (whole) p = h0 + k;
+    }
+    if (go && !(hay16 && whole)) p = first_in_line(hay, h0, std::min(h0 + CHUNK, n) - 1, x, before);
+    if (q < m) out[q] = p;
+  }
 }
 
 // INDEXED: the sampled search runs over the index lines and finishes with
-// one line of the index and one chunk of the haystack; otherwise it runs
-// over the haystack itself. LINES (indexed, items dividing 128 bytes, at
-// most SAMPLES lines of `lines`): the sample holds the last entry of every
-// 128-byte line of `lines` (step == CHUNK), and each level below is one
-// line read whole (count_before); the haystack chunk too when the haystack
-// is 16-byte aligned (hay16) and the chunk full.
-template <class K, class Cmp, bool UPPER, uint32_t SAMPLES, bool INDEXED, bool LINES>
+// one line of the index and one chunk of the haystack, each by binary search;
+// otherwise it runs over the haystack itself.
+template <class K, class Cmp, bool UPPER, uint32_t SAMPLES, bool INDEXED>
 __global__ void __launch_bounds__(THREADS)
 search_kernel(const K *__restrict__ hay, size_t n, const K *__restrict__ index, size_t chunks,
               const K *__restrict__ lines, size_t nlines, const K *__restrict__ needles,
-              size_t m, uint64_t *__restrict__ out, size_t step, bool hay16) {
+              size_t m, uint64_t *__restrict__ out, size_t step) {
   __shared__ K sample[SAMPLES];
   constexpr size_t CHUNK = chunk_items<K>();
   const Before<K, Cmp, UPPER> before{};
@@ -167,37 +264,6 @@ search_kernel(const K *__restrict__ hay, size_t n, const K *__restrict__ index, 
   for (size_t q = size_t(blockIdx.x) * THREADS + threadIdx.x; q < m;
        q += size_t(gridDim.x) * THREADS) {
     const K x = needles[q];
-    if constexpr (LINES && line_items<K>()) {
-      // Line L of `lines`: the first whose last entry is not before x (the
-      // sample holds the full lines' last entries; L == used is the partial
-      // last line, or past the end).
-      uint32_t lo = 0, hi = used;
-      while (lo < hi) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (before(sample[mid], x)) lo = mid + 1;
-        else hi = mid;
-      }
-      size_t p = n;
-      const size_t l0 = size_t(lo) * CHUNK;
-      if (l0 < nlines) {
-        const size_t j = l0 + count_before(lines + l0, uint32_t(std::min(CHUNK, nlines - l0)), x,
-                                           before);
-        if (j < nlines) {
-          const size_t i0 = j * CHUNK;
-          // Below chunks for a sorted haystack; clamped so that an unsorted
-          // one (unspecified results) still reads in bounds.
-          const size_t c = std::min(
-              chunks - 1,
-              i0 + count_before(index + i0, uint32_t(std::min(CHUNK, chunks - i0)), x, before));
-          const size_t h0 = c * CHUNK;
-          p = hay16 && h0 + CHUNK <= n
-                  ? h0 + count_before(hay + h0, uint32_t(CHUNK), x, before)
-                  : first_in_line(hay, h0, std::min(h0 + CHUNK, n) - 1, x, before);
-        }
-      }
-      out[q] = p;
-      continue;
-    }
     size_t p = first_not_before<K, Before<K, Cmp, UPPER>, SAMPLES>(arr, len, sample, used, step,
                                                                    x, before);
     if constexpr (INDEXED) {
@@ -297,24 +363,28 @@ rccl_hip_status run(const SearchArgs &a) {
       std::min<size_t>((a.m + THREADS - 1) / THREADS, size_t(cus) * BLOCKS_PER_CU)));
   KernelTimer t("search", a.stream, a.m);
   const K *needles = static_cast<const K *>(a.needles);
-  auto launch = [&](auto upper, auto idx, auto lines_mode) {
-    search_kernel<K, Cmp, decltype(upper)::value, SAMPLES, decltype(idx)::value,
-                  decltype(lines_mode)::value><<<grid, THREADS, 0, a.stream>>>(
-        hay, a.n, index, chunks, lines, nlines, needles, a.m, a.out, step, hay16);
+  auto launch = [&](auto upper, auto idx) {
+    search_kernel<K, Cmp, decltype(upper)::value, SAMPLES, decltype(idx)::value>
+        <<<grid, THREADS, 0, a.stream>>>(hay, a.n, index, chunks, lines, nlines, needles, a.m,
+                                         a.out, step);
   };
   using T = std::true_type;
   using F = std::false_type;
   if (line_search) {
     if constexpr (line_items<K>()) {
-      if (a.upper) launch(T{}, T{}, T{});
-      else launch(F{}, T{}, T{});
+      if (a.upper)
+        line_search_kernel<K, Cmp, true, SAMPLES><<<grid, THREADS, 0, a.stream>>>(
+            hay, a.n, index, chunks, lines, nlines, needles, a.m, a.out, hay16);
+      else
+        line_search_kernel<K, Cmp, false, SAMPLES><<<grid, THREADS, 0, a.stream>>>(
+            hay, a.n, index, chunks, lines, nlines, needles, a.m, a.out, hay16);
     }
   } else if (indexed) {
-    if (a.upper) launch(T{}, T{}, F{});
-    else launch(F{}, T{}, F{});
+    if (a.upper) launch(T{}, T{});
+    else launch(F{}, T{});
   } else {
-    if (a.upper) launch(T{}, F{}, F{});
-    else launch(F{}, F{}, F{});
+    if (a.upper) launch(T{}, F{});
+    else launch(F{}, F{});
   }
   return check_launch("search");
 }
