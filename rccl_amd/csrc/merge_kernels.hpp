@@ -255,8 +255,9 @@ rccl_hip_status run_merge(const MergeArgs &m) {
     {
       KernelTimer t("merge_sample", m.stream, ka);
       ordering::merge_sample_kernel<K, Cmp>
-          <<<dim3(static_cast<uint32_t>((ka + 255) / 256)), 256, 0, m.stream>>>(
-              static_cast<const K *>(m.a), m.na, static_cast<const K *>(m.b), m.nb, samples);
+          <<<dim3(static_cast<uint32_t>(ordering::merge_sample_blocks(m.na))), 256, 0,
+             m.stream>>>(static_cast<const K *>(m.a), m.na, static_cast<const K *>(m.b), m.nb,
+                         samples);
     }
     RCCL_HIP_TRY(check_launch("merge sample"));
     KernelTimer t("merge_partition", m.stream, tiles + 1);

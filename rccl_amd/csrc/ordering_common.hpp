@@ -134,24 +134,64 @@ constexpr bool sampled_partition_for() {
 // Samples of an A of `na` items (entries of the m array).
 __host__ __device__ inline size_t merge_samples(size_t na) { return (na + MERGE_SAMPLE - 1) / MERGE_SAMPLE; }
 
+// ---------------------------------------------------------------------------
+// Group searches. A search over HBM whose every probe is a dependent round
+// trip is latency-bound. The searches below run on the 8 lanes of an aligned
+// lane group, which all hold the same search: each round the lanes probe 8
+// evenly spaced points and a ballot counts those still before the answer, a
+// 9-ary search: about log9 of the range in dependent rounds instead of log2.
+// ---------------------------------------------------------------------------
+constexpr uint32_t SEARCH_GROUP = 8;
+
+// First x in [lo, hi) with !before(x), or hi, where `before` holds on a
+// prefix of the range (on any other predicate the result stays in [lo, hi]).
+// Every lane of the group calls it with the same arguments.
+template <class Before>
+__device__ __forceinline__ size_t group_first_not(size_t lo, size_t hi, Before before) {
+  const uint32_t lane = lane_id();
+  const uint32_t sub = lane & (SEARCH_GROUP - 1u), base = lane & ~(SEARCH_GROUP - 1u);
+  while (lo < hi) {
+    const size_t span = hi - lo;
+    if (span <= SEARCH_GROUP) {
+      const bool bf = sub < span && before(lo + sub);
+      return lo + __builtin_popcount(static_cast<uint32_t>(__ballot(bf) >> base) & 0xFFu);
+    }
+    const bool bf = before(lo + (size_t(sub) + 1) * span / 9);
+    const size_t cnt = __builtin_popcount(static_cast<uint32_t>(__ballot(bf) >> base) & 0xFFu);
+    // Probe j sits at lo + (j + 1) * span / 9: the answer lies after probe
+    // cnt - 1 and at or before probe cnt.
+    const size_t l0 = lo;
+    if (cnt > 0) lo = l0 + cnt * span / 9 + 1;
+    if (cnt < SEARCH_GROUP) hi = l0 + (cnt + 1) * span / 9;
+  }
+  return lo;
+}
+
+// Eight lanes per sample (group_first_not): with one sample per 2,048 items
+// the searches are few and latency-bound (C4: 0.016 -> 0.014 ms, C5 0.013-0.015
+// -> 0.010-0.011 ms against one thread per sample).
 template <class K, class Cmp>
 __global__ void __launch_bounds__(256)
 merge_sample_kernel(const K *__restrict__ a, size_t na, const K *__restrict__ b, size_t nb,
                     uint32_t *__restrict__ m_out) {
-  const size_t k = size_t(blockIdx.x) * 256 + threadIdx.x;
+  const size_t k = (size_t(blockIdx.x) * 256 + threadIdx.x) / SEARCH_GROUP;
   const size_t ka = merge_samples(na), kb = merge_samples(nb);
-  if (k >= ka) return;
+  if (k >= ka) return;  // whole groups
   const K x = a[k * MERGE_SAMPLE];
   const Cmp less{};
-  size_t lo = 0, hi = kb;  // first sampled B position not before x
-  while (lo < hi) {
-    const size_t mid = lo + (hi - lo) / 2;
-    if (less(b[mid * MERGE_SAMPLE], x)) lo = mid + 1; else hi = mid;
-  }
-  m_out[k] = static_cast<uint32_t>(lo);
+  // First sampled B position not before x.
+  const size_t lo =
+      group_first_not(0, kb, [&](size_t j) { return less(b[j * MERGE_SAMPLE], x); });
+  if (threadIdx.x % SEARCH_GROUP == 0) m_out[k] = static_cast<uint32_t>(lo);
+}
+inline size_t merge_sample_blocks(size_t na) {
+  return (merge_samples(na) * SEARCH_GROUP + 255) / 256;
 }
 
-// merge_path of diagonal d, searched in the window the samples allow.
+// merge_path of diagonal d, searched in the window the samples allow. One
+// thread per diagonal: with a boundary per merge tile (131,073 for C4) the
+// searches are bound by their random line reads, which a group search would
+// multiply (8 lanes per boundary: 0.069 -> 0.099 ms for C4).
 template <class K, class Cmp, class ReadA, class ReadB>
 __device__ __forceinline__ size_t sampled_merge_path(ReadA a, size_t na, ReadB b, size_t nb,
                                                      size_t d, const uint32_t *__restrict__ m,

@@ -642,8 +642,8 @@ rccl_hip_status run_op(const SetArgs &s) {
     {
       KernelTimer t("set_sample", s.stream, ka);
       ordering::merge_sample_kernel<K, Cmp>
-          <<<dim3(static_cast<uint32_t>((ka + 255) / 256)), 256, 0, s.stream>>>(a, s.na, b, s.nb,
-                                                                               m);
+          <<<dim3(static_cast<uint32_t>(ordering::merge_sample_blocks(s.na))), 256, 0,
+             s.stream>>>(a, s.na, b, s.nb, m);
     }
     RCCL_HIP_TRY(check_launch("set sample"));
   }
