@@ -197,9 +197,14 @@ constexpr size_t tile_items(size_t key_bytes, size_t value_bytes) {
 #ifndef RCCL_RADIX_SMALL_MAX_TILES
 #define RCCL_RADIX_SMALL_MAX_TILES 512
 #endif
+#ifndef RCCL_RADIX_SMALL_ITEMS_DIV
+#define RCCL_RADIX_SMALL_ITEMS_DIV 2
+#endif
 constexpr int SMALL_THREADS = RCCL_RADIX_SMALL_THREADS;
 constexpr int small_items_for(size_t key_bytes, size_t value_bytes) {
-  return items_for(key_bytes, value_bytes) / 2 > 0 ? items_for(key_bytes, value_bytes) / 2 : 1;
+  return items_for(key_bytes, value_bytes) / RCCL_RADIX_SMALL_ITEMS_DIV > 0
+             ? items_for(key_bytes, value_bytes) / RCCL_RADIX_SMALL_ITEMS_DIV
+             : 1;
 }
 constexpr size_t small_tile_items(size_t key_bytes, size_t value_bytes) {
   return size_t(SMALL_THREADS) * small_items_for(key_bytes, value_bytes);
