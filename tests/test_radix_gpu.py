@@ -411,3 +411,28 @@ def test_tile_shape_threshold(launch, kind, width, side, descending):
         gk, gv = _sort_pairs(launch, keys, values, descending)
         np.testing.assert_array_equal(_bits(gk), _bits(wk))
         assert np.array_equal(gv, wv)
+
+
+@pytest.mark.parametrize("tiles", [1, 2, 15, 16, 17, 64, 241, 511])
+@pytest.mark.parametrize("delta", [-1, 0, 1])
+def test_small_tile_counts(launch, tiles, delta):
+    """Plain sorts whose small-tile count lands on, just below and just past
+    multiples of the tile (look-back groups of 16, XCD runs of 8): keys and
+    u64 + u32 pairs against the oracle."""
+    for kb, vb, kind in ((4, 0, "u32"), (8, 4, "u64")):
+        tile = radix_shapes.SMALL_THREADS * max(1, radix_shapes.items(kb, vb) // 2)
+        n = tiles * tile + delta
+        if n < 1 or n > radix_shapes.small_tile_max(kb, vb):
+            continue
+        raw = workloads.hash_range(0x7A11 + tiles * 7 + delta, n)
+        if vb == 0:
+            keys = (raw >> np.uint64(40)).astype(np.uint32)  # 24-bit keys: ties
+            np.testing.assert_array_equal(_sort_keys(launch, keys),
+                                          oracle.radix_sort(kind, keys))
+        else:
+            keys = raw >> np.uint64(20)
+            values = np.arange(n, dtype=np.uint32)
+            gk, gv = _sort_pairs(launch, keys, values)
+            wk, wv = oracle.radix_sort(kind, keys, values)
+            np.testing.assert_array_equal(gk, wk)
+            np.testing.assert_array_equal(gv, wv)
