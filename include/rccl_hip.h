@@ -175,7 +175,9 @@ RCCL_HIP_API rccl_hip_status rccl_hip_radix_sort_workspace_bytes(rccl_hip_key_ki
  * Replaces device_radix_sort_{keys,pairs}_buffer{,_descending}
  * (rccl-cub/src/dispatch.rs:2091-2943; pass control rccl-cub/src/radix.rs:427-554,
  * :627-759; DoubleBuffer rccl-cub/src/double_buffer.rs:6-130). Stable; no
- * length cap below 2^32 items. */
+ * length cap below 2^32 items. The four buffers must not share a byte
+ * (RCCL_HIP_ERROR_INVALID_ARGUMENT before any launch): every pass reads one of
+ * each pair and writes the other. */
 RCCL_HIP_API rccl_hip_status rccl_hip_radix_sort_buffer(rccl_hip_key_kind key, size_t value_bytes,
                                            rccl_hip_order order, void *keys_first,
                                            void *keys_second, void *values_first,
@@ -238,7 +240,8 @@ RCCL_HIP_API rccl_hip_status rccl_hip_radix_sort_static(rccl_hip_key_kind key,
 /* In-place radix sort of all key bits with caller-owned scratch of n keys
  * (and n values). Replaces device_radix_sort_{keys,pairs}{,_descending}
  * (rccl-cub/src/radix.rs:558-623, :763-876): the result is copied back when
- * it lands in the scratch buffer. */
+ * it lands in the scratch buffer. keys, values and the scratch buffers must
+ * not share a byte (RCCL_HIP_ERROR_INVALID_ARGUMENT). */
 RCCL_HIP_API rccl_hip_status rccl_hip_radix_sort(rccl_hip_key_kind key, size_t value_bytes,
                                     rccl_hip_order order, void *keys, void *values,
                                     void *scratch_keys, void *scratch_values, size_t n,
@@ -258,7 +261,9 @@ RCCL_HIP_API rccl_hip_status rccl_hip_merge_workspace_bytes(rccl_hip_key_kind ke
  * keys every item of A precedes those of B. Values (value_bytes > 0) follow
  * their keys. Replaces device_merge_keys/device_merge_pairs
  * (rccl-cub/src/dispatch.rs:1572,1915; rccl-cub/src/merge.rs:194-368) and the
- * Thrust merge(..).write_into forms (rccl-thrust/src/merge.rs:83-247). */
+ * Thrust merge(..).write_into forms (rccl-thrust/src/merge.rs:83-247). An
+ * output that shares a byte with an input, or out_keys with out_values, is
+ * rejected with RCCL_HIP_ERROR_INVALID_ARGUMENT. */
 RCCL_HIP_API rccl_hip_status rccl_hip_merge(rccl_hip_key_kind key, size_t value_bytes,
                                rccl_hip_order order, const void *a_keys,
                                const void *a_values, size_t na, const void *b_keys,
@@ -278,7 +283,9 @@ RCCL_HIP_API rccl_hip_status rccl_hip_merge_sort_workspace_bytes(rccl_hip_key_ki
                                                     size_t *bytes);
 
 /* Stable merge sort. in_keys == out_keys (and in_values == out_values) sorts
- * in place; otherwise the inputs are left untouched (the _copy forms). Float
+ * in place; otherwise the inputs are left untouched (the _copy forms), and an
+ * output that partly overlaps its input (or out_keys that overlaps
+ * out_values) is rejected with RCCL_HIP_ERROR_INVALID_ARGUMENT. Float
  * keys compare with IEEE `<` (-0.0 and +0.0 are equal and keep their input
  * order); inputs holding NaN, which `<` cannot order, have no defined order.
  * Replaces device_merge_sort_{keys,pairs}{,_copy}
@@ -339,6 +346,8 @@ RCCL_HIP_API rccl_hip_status rccl_hip_set_op_workspace_bytes(rccl_hip_set_operat
  * the number of items out_keys (and out_values) can hold: the full result
  * length is always counted, but items at or past out_capacity are not
  * written (the reference leaves the destination's size to the caller).
+ * Outputs (out_capacity items) that share a byte with an input it reads are
+ * rejected with RCCL_HIP_ERROR_INVALID_ARGUMENT.
  * Replaces Launch::set_keys / set_pairs (rccl-cub/src/dispatch.rs:413-550;
  * rccl-cub/src/set_operation.rs:265-589) and the Thrust union/intersection/
  * difference/symmetric_difference expressions (rccl-thrust/src/set.rs:357-898). */

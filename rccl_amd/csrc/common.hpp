@@ -46,6 +46,33 @@ private:
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Whether the byte ranges [a, a + an) and [b, b + bn) share a byte (empty or
+// null ranges share none).
+inline bool ranges_overlap(const void *a, size_t an, const void *b, size_t bn) {
+  if (!a || !b || an == 0 || bn == 0) return false;
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x >= y ? x - y < bn : y - x < an;  // no sum that could wrap
+}
+
+// a * b, or SIZE_MAX where that overflows (byte counts of huge capacities).
+inline size_t sat_mul(size_t a, size_t b) { return b && a > SIZE_MAX / b ? SIZE_MAX : a * b; }
+
+// Whether any output range shares a byte with any input range: kernels that
+// read their inputs tile by tile while writing their outputs elsewhere
+// (merge, set operations) would race on such a call. The reference's borrows
+// rule it out; through the C ABI it is rejected before any launch.
+struct ByteRange {
+  const void *p;
+  size_t bytes;
+};
+template <size_t NO, size_t NI>
+inline bool outputs_overlap_inputs(const ByteRange (&outs)[NO], const ByteRange (&ins)[NI]) {
+  for (const ByteRange &o : outs)
+    for (const ByteRange &i : ins)
+      if (ranges_overlap(o.p, o.bytes, i.p, i.bytes)) return true;
+  return false;
+}
+
 // Blocks of `kernel` (launched with `threads` threads and no dynamic LDS) that
 // the current device holds at once: CUs x resident blocks per CU. Cached per
 // device and kernel.

@@ -137,6 +137,15 @@ rccl_hip_status rccl_hip_merge(rccl_hip_key_kind key, size_t value_bytes, rccl_h
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "merge keys");
   if (value_bytes && ((na && !a_values) || (nb && !b_values) || !out_values))
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "merge values");
+  {
+    const size_t kb = key_bytes(key), n = na + nb, vb = value_bytes;
+    const ByteRange outs[] = {{out_keys, sat_mul(n, kb)}, {out_values, sat_mul(n, vb)}};
+    const ByteRange ins[] = {{a_keys, sat_mul(na, kb)}, {b_keys, sat_mul(nb, kb)},
+                             {a_values, sat_mul(na, vb)}, {b_values, sat_mul(nb, vb)}};
+    if (outputs_overlap_inputs(outs, ins) ||
+        ranges_overlap(out_keys, sat_mul(n, kb), out_values, sat_mul(n, vb)))
+      return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "merge output overlaps an input");
+  }
   merge::MergeArgs m{a_keys, a_values, b_keys, b_values, na, nb, out_keys, out_values,
                      workspace, workspace_bytes, stream};
   return merge_run(key, m, value_bytes, order == RCCL_HIP_ORDER_DESCENDING);
@@ -159,6 +168,15 @@ rccl_hip_status rccl_hip_merge_sort(rccl_hip_key_kind key, size_t value_bytes, r
   if (!in_keys || !out_keys) return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "merge sort keys");
   if (value_bytes && (!in_values || !out_values))
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "merge sort values");
+  {
+    // Each stream is sorted in place (input == output) or into a disjoint
+    // output; a partly overlapping one would be read and written by one pass.
+    const size_t kb = sat_mul(key_bytes(key), n), vb = sat_mul(value_bytes, n);
+    if ((in_keys != out_keys && ranges_overlap(in_keys, kb, out_keys, kb)) ||
+        (value_bytes && in_values != out_values && ranges_overlap(in_values, vb, out_values, vb)) ||
+        ranges_overlap(out_keys, kb, out_values, vb))
+      return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "merge sort buffers overlap");
+  }
   if (lowers_to_radix(key, n))
     return radix::merge_sort_lowering(key, value_bytes, order == RCCL_HIP_ORDER_DESCENDING,
                                       in_keys, in_values, out_keys, out_values, n, workspace,

@@ -232,6 +232,18 @@ rccl_hip_status sort_buffer(rccl_hip_key_kind key, size_t value_bytes, rccl_hip_
   if (!a.keys[0] || !a.keys[1]) return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix keys");
   if (value_bytes && (!a.vals[0] || !a.vals[1]))
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix values");
+  if (!a.planned) {
+    // Every pass reads one buffer of each pair and writes the other: the
+    // four buffers must not share a byte (the reference's borrows make them
+    // distinct; here an aliased scratch would race silently).
+    const size_t kb = key_bytes(key) * a.n, vb = value_bytes * a.n;
+    const void *p[4] = {a.keys[0], a.keys[1], a.vals[0], a.vals[1]};
+    const size_t s[4] = {kb, kb, vb, vb};
+    for (int i = 0; i < 4; ++i)
+      for (int j = i + 1; j < 4; ++j)
+        if (ranges_overlap(p[i], s[i], p[j], s[j]))
+          return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix buffers overlap");
+  }
   const Layout l = layout(key_bytes(key), value_bytes, a.n, a.planned);
   if (!a.ws || workspace_bytes < l.total)
     return set_error(RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL, "radix workspace", l.total,

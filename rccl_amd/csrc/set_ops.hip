@@ -105,6 +105,16 @@ rccl_hip_status rccl_hip_set_op(rccl_hip_set_operation op, rccl_hip_key_kind key
       op == RCCL_HIP_SET_UNION || op == RCCL_HIP_SET_SYMMETRIC_DIFFERENCE;
   if (vb && ((na && !a_values) || (reads_b_values && nb && !b_values) || !out_values))
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "set values");
+  if (out_keys) {
+    const size_t kb = key_bytes(key), cap = out_capacity;
+    const ByteRange outs[] = {{out_keys, sat_mul(cap, kb)}, {out_values, sat_mul(cap, vb)}};
+    const ByteRange ins[] = {{a_keys, sat_mul(na, kb)}, {b_keys, sat_mul(nb, kb)},
+                             {a_values, sat_mul(na, vb)},
+                             {reads_b_values ? b_values : nullptr, sat_mul(nb, vb)}};
+    if (outputs_overlap_inputs(outs, ins) ||
+        ranges_overlap(out_keys, sat_mul(cap, kb), out_values, sat_mul(cap, vb)))
+      return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "set output overlaps an input");
+  }
   set_ops::SetArgs s{};
   s.op = static_cast<int>(op);
   s.a = a_keys;

@@ -19,6 +19,8 @@ from rccl_amd.device import KIND_DTYPES, kind_of
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "rccl_hip.h")
 FAKE = ctypes.c_void_p(4096)  # never dereferenced: every call below fails validation first
+# Distinct fake buffers, 4 GiB apart, where a call must pass the overlap checks.
+P1, P2, P3, P4 = (ctypes.c_void_p(k << 32) for k in (1, 2, 3, 4))
 
 
 @pytest.fixture(scope="module")
@@ -70,7 +72,7 @@ def test_radix_validation_before_launch(lib):
         assert (info.begin_bit, info.end_bit, info.key_bits) == (begin, end, 32)
     # A workspace smaller than required reports both sizes.
     need = _abi.workspace_bytes("rccl_hip_radix_sort_workspace_bytes", 0, 0, 1000)
-    rc = lib.rccl_hip_radix_sort_buffer(0, 0, 0, FAKE, FAKE, None, None, 1000, ctypes.byref(cur),
+    rc = lib.rccl_hip_radix_sort_buffer(0, 0, 0, P1, P2, None, None, 1000, ctypes.byref(cur),
                                         0, 32, FAKE, need - 1, None)
     assert rc == 2
     info = _last()
@@ -81,19 +83,64 @@ def test_radix_validation_before_launch(lib):
     assert lib.rccl_hip_radix_sort_workspace_bytes(0, 3, 10, ctypes.byref(out)) == 9
 
 
+def _ptr(x):
+    return ctypes.c_void_p(x)
+
+
+def test_overlapping_buffers_rejected(lib):
+    """Buffers a kernel would read and write in one pass are rejected before
+    any launch (the reference's borrows rule them out; through the C ABI a
+    caller could pass them). Pointers are never dereferenced: every call fails
+    validation, and the accepted layouts fail later on a short workspace."""
+    base = 1 << 32
+    cur = ctypes.c_int(1)
+    n = 1000  # u32 keys: 4,000 bytes
+    # Radix double buffer: aliased or partly overlapping halves (keys or values).
+    for k1, k2, v1, v2 in [(base, base, None, None), (base, base + 4, None, None),
+                           (base, base + 8192, base + 100, base + 20000),
+                           (base, base + 8192, base + 16384, base + 16384 + 16)]:
+        vb = 0 if v1 is None else 4
+        rc = lib.rccl_hip_radix_sort_buffer(0, vb, 0, _ptr(k1), _ptr(k2),
+                                            None if v1 is None else _ptr(v1),
+                                            None if v2 is None else _ptr(v2), n,
+                                            ctypes.byref(cur), 0, 32, FAKE, 1 << 20, None)
+        assert rc == 9 and _last().role == b"radix buffers overlap"
+    # Disjoint halves pass that check and stop at the workspace.
+    assert lib.rccl_hip_radix_sort_buffer(0, 0, 0, _ptr(base), _ptr(base + 4000), None, None, n,
+                                          ctypes.byref(cur), 0, 32, FAKE, 1, None) == 2
+    # In-place radix sort whose scratch is the keys.
+    assert lib.rccl_hip_radix_sort(0, 0, 0, _ptr(base), None, _ptr(base), None, n, FAKE,
+                                   1 << 20, None) == 9
+    # Merge: an output over an input.
+    assert lib.rccl_hip_merge(0, 0, 0, _ptr(base), None, n, _ptr(base + 8192), None, n,
+                              _ptr(base + 8192 + 400), None, FAKE, 1 << 20, None) == 9
+    assert _last().role == b"merge output overlaps an input"
+    # Merge sort: a partly overlapping output is rejected; in place is not.
+    assert lib.rccl_hip_merge_sort(0, 0, 0, _ptr(base), None, _ptr(base + 4), None, 100_000,
+                                   FAKE, 1 << 30, None) == 9
+    assert lib.rccl_hip_merge_sort(0, 0, 0, _ptr(base), None, _ptr(base), None, 100_000,
+                                   FAKE, 1, None) == 2
+    # Set operations: an output over the second input, even with a huge capacity.
+    for cap in (2 * n, (1 << 64) - 1):
+        assert lib.rccl_hip_set_op(0, 0, 0, 0, _ptr(base), None, n, _ptr(base + 8192), None, n,
+                                   _ptr(base + 8192 + 4 * (n - 1)), None, cap, FAKE, FAKE,
+                                   1 << 20, None) == 9
+        assert _last().role == b"set output overlaps an input"
+
+
 def test_merge_and_sort_validation(lib):
     huge = (1 << 64) - 1
     assert lib.rccl_hip_merge(0, 0, 0, FAKE, None, huge, FAKE, None, 2, FAKE, None, FAKE, 1,
                               None) == 5  # SizeOverflow
     need = _abi.workspace_bytes("rccl_hip_merge_workspace_bytes", 0, 0, 50_000, 50_000)
-    assert lib.rccl_hip_merge(0, 0, 0, FAKE, None, 50_000, FAKE, None, 50_000, FAKE, None, FAKE,
+    assert lib.rccl_hip_merge(0, 0, 0, P1, None, 50_000, P2, None, 50_000, P3, None, FAKE,
                               need - 1, None) == 2
     assert lib.rccl_hip_merge(0, 4, 0, FAKE, None, 10, FAKE, None, 10, FAKE, None, FAKE,
                               need, None) == 9  # values missing
     assert lib.rccl_hip_merge(0, 0, 0, None, None, 0, None, None, 0, None, None, None, 0,
                               None) == 0  # empty: nothing to do
     need = _abi.workspace_bytes("rccl_hip_merge_sort_workspace_bytes", 3, 8, 100_000)
-    assert lib.rccl_hip_merge_sort(3, 8, 0, FAKE, FAKE, FAKE, FAKE, 100_000, FAKE, need - 1,
+    assert lib.rccl_hip_merge_sort(3, 8, 0, P1, P2, P3, P4, 100_000, FAKE, need - 1,
                                    None) == 2
     assert lib.rccl_hip_merge_sort(3, 8, 2, FAKE, FAKE, FAKE, FAKE, 10, FAKE, need, None) == 9
 
@@ -104,7 +151,7 @@ def test_set_validation(lib):
     assert lib.rccl_hip_set_op(0, 0, 0, 0, FAKE, None, 10, FAKE, None, 10, None, None, 0, None,
                                FAKE, 1 << 20, None) == 9  # count-only needs a count
     need = _abi.workspace_bytes("rccl_hip_set_op_workspace_bytes", 0, 3, 0, 1 << 20, 1 << 20)
-    assert lib.rccl_hip_set_op(0, 3, 0, 0, FAKE, None, 1 << 20, FAKE, None, 1 << 20, FAKE, None,
+    assert lib.rccl_hip_set_op(0, 3, 0, 0, P1, None, 1 << 20, P2, None, 1 << 20, P3, None,
                                1 << 21, FAKE, FAKE, need - 1, None) == 2
     # Union reads the second range's values; intersection does not.
     assert lib.rccl_hip_set_op(0, 0, 4, 0, FAKE, FAKE, 10, FAKE, None, 10, FAKE, FAKE, 20, FAKE,
@@ -273,8 +320,8 @@ def test_merge_sort_radix_lowering_workspace(lib, key, kb, vb):
             align(65_535 * kb) + align(65_535 * vb) + radix
     # Too small a workspace fails before any launch.
     need = _abi.workspace_bytes("rccl_hip_merge_sort_workspace_bytes", key, vb, 70_000)
-    assert lib.rccl_hip_merge_sort(key, vb, 0, FAKE, FAKE if vb else None, FAKE,
-                                   FAKE if vb else None, 70_000, FAKE, need - 1, None) == 2
+    assert lib.rccl_hip_merge_sort(key, vb, 0, P1, P2 if vb else None, P1,
+                                   P2 if vb else None, 70_000, FAKE, need - 1, None) == 2
 
 
 @pytest.mark.parametrize("key,kb", [(0, 4), (3, 8)])
