@@ -319,7 +319,9 @@ RCCL_HIP_API rccl_hip_status rccl_hip_record_sort_workspace_bytes(uint32_t arity
  * rows the sort is a multi-word LSD radix sort whose ranking relies on the
  * check rccl_hip_program_load runs, so load the device first. Replaces
  * sort_rows_lexicographic{,_into} and sort_rows_with_payload_lexicographic{,_into}
- * (rccl-thrust/src/record_sort.rs:144-366). */
+ * (rccl-thrust/src/record_sort.rs:144-366). Outputs that partly overlap their inputs,
+ * or out_rows that overlaps out_payloads, are rejected with
+ * RCCL_HIP_ERROR_INVALID_ARGUMENT. */
 RCCL_HIP_API rccl_hip_status rccl_hip_record_sort(uint32_t arity, size_t payload_bytes,
                                      const void *in_rows, const void *in_payloads,
                                      void *out_rows, void *out_payloads, size_t n,
@@ -394,7 +396,7 @@ RCCL_HIP_API rccl_hip_status rccl_hip_group_workspace_bytes(rccl_hip_key_kind ke
 /* Stable adjacent unique: out_keys[0, count) (and out_payloads) = the first
  * item of every run of in_keys[0, n); count is written to *d_count (device
  * memory, one uint64_t). Outputs must hold n items and not overlap the
- * inputs. Replaces unique_copy_by (rccl-thrust/src/compaction.rs:224-301)
+ * inputs or each other (RCCL_HIP_ERROR_INVALID_ARGUMENT). Replaces unique_copy_by (rccl-thrust/src/compaction.rs:224-301)
  * with the natural equivalence; the in-place unique_by (:303-378) is a copy
  * to the scratch range followed by this call from the scratch back into the
  * values. */
@@ -410,8 +412,8 @@ RCCL_HIP_API rccl_hip_status rccl_hip_unique_copy(rccl_hip_key_kind key, uint32_
  * left fold ((v0 op v1) op v2) ... of its values, in run order; the number of
  * runs is written to *d_group_count. op is NATURAL_BAG_ADD (u64 values),
  * BOOLEAN_OR (1-byte values) or INDEPENDENT_PROBABILITY_OR (f64 values).
- * Outputs must hold n items and not overlap the inputs. Replaces
- * reduce_by_key (rccl-thrust/src/grouped_reduction.rs:102-216,
+ * Outputs must hold n items and not overlap the inputs or each other
+ * (RCCL_HIP_ERROR_INVALID_ARGUMENT). Replaces reduce_by_key (rccl-thrust/src/grouped_reduction.rs:102-216,
  * rccl-cub/src/grouped_reduction.rs:83-143) with the natural equivalence. */
 RCCL_HIP_API rccl_hip_status rccl_hip_reduce_by_key(
     rccl_hip_key_kind key, uint32_t arity, rccl_hip_group_op op, size_t payload_bytes,
@@ -431,7 +433,8 @@ RCCL_HIP_API rccl_hip_status rccl_hip_reduce_by_key(
  * reverse when order is DESCENDING); with arity 2..6 and key == U32 the
  * items are [u32; arity] rows in ascending lexicographic order. The haystack
  * must be sorted under that order (results are unspecified otherwise, as
- * with NaN keys). thrust::lower_bound / upper_bound over a range of values
+ * with NaN keys). out_indices must not overlap the haystack or the needles
+ * (RCCL_HIP_ERROR_INVALID_ARGUMENT). thrust::lower_bound / upper_bound over a range of values
  * has no counterpart in the reference (CCCL_RUST_CAPABILITY_CHECKLIST.md:107
  * lists it as missing); its datalog callers search sorted columns.
  * The workspace (rccl_hip_bound_search_workspace_bytes) holds a per-call

@@ -92,6 +92,14 @@ rccl_hip_status run_for(int slot, const group::GroupArgs &a, rccl_hip_group_op o
   }
 }
 
+// Bytes of one key ([u32; arity] rows from arity 2) and of one reduced value.
+size_t key_item_bytes(rccl_hip_key_kind key, uint32_t arity) {
+  return arity > 1 ? 4u * size_t(arity) : key_bytes(key);
+}
+size_t value_item_bytes(rccl_hip_group_op op) {
+  return op == RCCL_HIP_GROUP_BOOLEAN_OR ? 1u : 8u;
+}
+
 } // namespace
 
 extern "C" {
@@ -118,6 +126,13 @@ rccl_hip_status rccl_hip_unique_copy(rccl_hip_key_kind key, uint32_t arity, size
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "unique keys");
   if (n && payload_bytes && (!in_payloads || !out_payloads))
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "unique payloads");
+  {
+    const size_t kb = sat_mul(n, key_item_bytes(key, arity)), pb = sat_mul(n, payload_bytes);
+    const ByteRange outs[] = {{out_keys, kb}, {out_payloads, pb}};
+    const ByteRange ins[] = {{in_keys, kb}, {in_payloads, pb}};
+    if (outputs_overlap_inputs(outs, ins) || ranges_overlap(out_keys, kb, out_payloads, pb))
+      return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "unique output overlaps an input");
+  }
   const group::GroupArgs a{in_keys, in_payloads, nullptr, out_keys, out_payloads, nullptr,
                            n, d_count, workspace, workspace_bytes, stream};
   return run_for(slot, a, RCCL_HIP_GROUP_UNIQUE, payload_bytes);
@@ -139,6 +154,16 @@ rccl_hip_status rccl_hip_reduce_by_key(rccl_hip_key_kind key, uint32_t arity,
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "reduce-by-key ranges");
   if (n && payload_bytes && (!key_payloads || !out_key_payloads))
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "reduce-by-key key payloads");
+  {
+    const size_t kb = sat_mul(n, key_item_bytes(key, arity)), pb = sat_mul(n, payload_bytes),
+                 vb = sat_mul(n, value_item_bytes(op));
+    const ByteRange outs[] = {{out_keys, kb}, {out_key_payloads, pb}, {out_values, vb}};
+    const ByteRange ins[] = {{keys, kb}, {key_payloads, pb}, {values, vb}};
+    if (outputs_overlap_inputs(outs, ins) || ranges_overlap(out_keys, kb, out_key_payloads, pb) ||
+        ranges_overlap(out_keys, kb, out_values, vb) ||
+        ranges_overlap(out_key_payloads, pb, out_values, vb))
+      return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "reduce-by-key output overlaps");
+  }
   const group::GroupArgs a{keys,     key_payloads,     values,        out_keys,
                            out_key_payloads, out_values, n, d_group_count,
                            workspace, workspace_bytes, stream};

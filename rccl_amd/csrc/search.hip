@@ -99,6 +99,13 @@ rccl_hip_status rccl_hip_bound_search(rccl_hip_key_kind key, uint32_t arity, rcc
   if (m && (!needles || !out_indices))
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "search needles or output");
   if (m && n && !haystack) return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "search haystack");
+  {
+    const size_t item = arity > 1 ? 4u * size_t(arity) : key_bytes(key);
+    const ByteRange outs[] = {{out_indices, sat_mul(m, sizeof(uint64_t))}};
+    const ByteRange ins[] = {{haystack, sat_mul(n, item)}, {needles, sat_mul(m, item)}};
+    if (outputs_overlap_inputs(outs, ins))
+      return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "search output overlaps an input");
+  }
   const search::SearchArgs a{haystack, needles, n,         m, out_indices, upper != 0,
                             workspace, workspace_bytes, stream};
   return dispatch(key, arity, order == RCCL_HIP_ORDER_DESCENDING, a);

@@ -128,6 +128,34 @@ def test_overlapping_buffers_rejected(lib):
         assert _last().role == b"set output overlaps an input"
 
 
+def test_overlapping_buffers_rejected_other_calls(lib):
+    """The same rule for compaction, bound search and record sort."""
+    base = 1 << 32
+    cnt = _ptr(base + (1 << 30))
+    n = 1000  # u32 keys: 4,000 bytes; u64 values: 8,000 bytes
+    # unique_copy: output keys over the input keys, or over the output payloads.
+    assert lib.rccl_hip_unique_copy(0, 1, 0, _ptr(base), None, _ptr(base + 2000), None, n, cnt,
+                                    FAKE, 1 << 20, None) == 9
+    assert _last().role == b"unique output overlaps an input"
+    assert lib.rccl_hip_unique_copy(0, 1, 8, _ptr(base), _ptr(base + 8192), _ptr(base + 20000),
+                                    _ptr(base + 20000 + 3996), n, cnt, FAKE, 1 << 20, None) == 9
+    # reduce_by_key (u64 NaturalBagAdd values): output values over the input values.
+    assert lib.rccl_hip_reduce_by_key(0, 1, 1, 0, _ptr(base), None, _ptr(base + 8192),
+                                      _ptr(base + 20000), None, _ptr(base + 8192 + 7992), n, cnt,
+                                      FAKE, 1 << 20, None) == 9
+    assert _last().role == b"reduce-by-key output overlaps"
+    # Bound search: indices over the needles.
+    assert lib.rccl_hip_bound_search(0, 1, 0, 0, _ptr(base), n, _ptr(base + 8192), n,
+                                     _ptr(base + 8192 + 16), FAKE, 1 << 20, None) == 9
+    assert _last().role == b"search output overlaps an input"
+    # Record sort: rows out partly over rows in; in place is accepted.
+    assert lib.rccl_hip_record_sort(4, 0, _ptr(base), None, _ptr(base + 16), None, 100_000,
+                                    FAKE, 1 << 30, None) == 9
+    assert _last().role == b"record-sort buffers overlap"
+    assert lib.rccl_hip_record_sort(4, 8, _ptr(base), _ptr(base + (1 << 28)), _ptr(base),
+                                    _ptr(base + (1 << 28)), 100_000, FAKE, 1, None) == 2
+
+
 def test_merge_and_sort_validation(lib):
     huge = (1 << 64) - 1
     assert lib.rccl_hip_merge(0, 0, 0, FAKE, None, huge, FAKE, None, 2, FAKE, None, FAKE, 1,
@@ -212,7 +240,7 @@ def test_group_validation(lib):
     assert lib.rccl_hip_group_workspace_bytes(0, 1, 0, 16, 100, ctypes.byref(out)) == 9
     need = _abi.workspace_bytes("rccl_hip_group_workspace_bytes", 0, 1, 1, 0, 1 << 20)
     assert 0 < need < (1 << 20)  # look-back state only
-    assert lib.rccl_hip_reduce_by_key(0, 1, 1, 0, FAKE, None, FAKE, FAKE, None, FAKE, 1 << 20,
+    assert lib.rccl_hip_reduce_by_key(0, 1, 1, 0, P1, None, P2, P3, None, P4, 1 << 20,
                                       FAKE, FAKE, need - 1, None) == 2
     assert lib.rccl_hip_reduce_by_key(0, 1, 0, 0, FAKE, None, FAKE, FAKE, None, FAKE, 10, FAKE,
                                       FAKE, need, None) == 9  # UNIQUE is not a reduction
@@ -236,7 +264,7 @@ def test_record_sort_validation(lib):
         assert lib.rccl_hip_record_sort_workspace_bytes(3, width, 10, ctypes.byref(out)) == 9
     need = _abi.workspace_bytes("rccl_hip_record_sort_workspace_bytes", 4, 8, 100_000)
     assert need >= 100_000 * (16 + 8)  # scratch rows and payloads
-    assert lib.rccl_hip_record_sort(4, 8, FAKE, FAKE, FAKE, FAKE, 100_000, FAKE, need - 1,
+    assert lib.rccl_hip_record_sort(4, 8, P1, P2, P1, P2, 100_000, FAKE, need - 1,
                                     None) == 2
     assert (_last().expected, _last().actual) == (need, need - 1)
     assert lib.rccl_hip_record_sort(4, 8, FAKE, None, FAKE, FAKE, 10, FAKE, need, None) == 9
@@ -436,9 +464,9 @@ def test_bound_search_workspace_and_validation(lib):
     assert lib.rccl_hip_bound_search_workspace_bytes(42, 1, 10, ctypes.byref(out)) == 9
     n, m = 1 << 26, 1 << 20
     need = ws(0, 1, n)
-    assert lib.rccl_hip_bound_search(0, 1, 0, 0, FAKE, n, FAKE, m, FAKE, FAKE, need - 1,
+    assert lib.rccl_hip_bound_search(0, 1, 0, 0, P1, n, P2, m, P3, FAKE, need - 1,
                                      None) == 2
-    assert lib.rccl_hip_bound_search(0, 1, 0, 0, FAKE, n, FAKE, m, FAKE, None, 0, None) == 2
+    assert lib.rccl_hip_bound_search(0, 1, 0, 0, P1, n, P2, m, P3, None, 0, None) == 2
     assert lib.rccl_hip_bound_search(0, 1, 0, 0, FAKE, n, FAKE, 0, FAKE, None, 0, None) == 0
 
 
