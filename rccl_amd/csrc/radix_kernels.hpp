@@ -40,20 +40,46 @@ struct KeyOps {
   static constexpr int NBITS = int(sizeof(Bits) * 8);
   static constexpr Bits SIGN = Bits(1) << (NBITS - 1);
 
-  __device__ static __forceinline__ Bits digit_source(Bits raw) {
+  // The order-preserving bijection, before the collapse. Onesweep passes keep
+  // keys in this form between passes: the first converts its raw input
+  // (image), the last its output back (raw), and every digit in between
+  // needs only the collapse (image_digit): about half the ALU work per digit
+  // for float keys.
+  __device__ static __forceinline__ Bits image(Bits raw) {
     Bits x = raw;
     if constexpr (KC == KeyClass::Signed) x ^= SIGN;
     if constexpr (KC == KeyClass::Float)
       x ^= static_cast<Bits>(static_cast<SBits>(raw) >> (NBITS - 1)) | SIGN;
     if constexpr (DESC) x = ~x;
-    if constexpr (KC == KeyClass::Float) x = (x == SIGN - 1) ? SIGN : x;
     return x;
   }
+  __device__ static __forceinline__ Bits raw(Bits x) {
+    if constexpr (DESC) x = ~x;
+    if constexpr (KC == KeyClass::Signed) x ^= SIGN;
+    // A set top bit marks a non-negative float (sign flipped), a clear one a
+    // negative float (all bits inverted).
+    if constexpr (KC == KeyClass::Float)
+      x ^= static_cast<Bits>(~(static_cast<SBits>(x) >> (NBITS - 1))) | SIGN;
+    return x;
+  }
+  __device__ static __forceinline__ Bits collapse(Bits x) {
+    if constexpr (KC == KeyClass::Float) return x == SIGN - 1 ? SIGN : x;
+    else return x;
+  }
+
+  __device__ static __forceinline__ Bits digit_source(Bits raw) { return collapse(image(raw)); }
 
   __device__ static __forceinline__ uint32_t digit(Bits raw, uint32_t bit, uint32_t mask) {
     return static_cast<uint32_t>(digit_source(raw) >> bit) & mask;
   }
+  __device__ static __forceinline__ uint32_t image_digit(Bits y, uint32_t bit, uint32_t mask) {
+    return static_cast<uint32_t>(collapse(y) >> bit) & mask;
+  }
 };
+
+// Conversion flags of one onesweep launch: its input is raw keys (convert
+// after loading), its output must be raw keys (convert before storing).
+constexpr uint32_t CONV_IN = 1u, CONV_OUT = 2u;
 
 // Key loads of a keys-only onesweep are non-temporal: they are read once, and
 // leaving L2 to the scattered writes (whose partial lines merge there) and the
@@ -327,7 +353,7 @@ histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__
 // 2 the scratch; lb is the look-back buffer of the pass (the active passes
 // alternate, starting with buffer 0, which the histogram zeroes).
 struct PassPlan {
-  uint32_t active, src, dst, lb;
+  uint32_t active, src, dst, lb, conv;  // conv: CONV_IN on the first active pass, CONV_OUT on the last
 };
 
 // Plan flags: some stream (keys or values) is sorted in place (input ==
@@ -362,10 +388,11 @@ __device__ inline void assign_plan(int P, uint32_t trivial, uint32_t flags,
   }
   uint32_t j = 0, prev = 0;
   for (int p = 0; p < P; ++p) {
-    PassPlan e{0u, 0u, 0u, 0u};
+    PassPlan e{0u, 0u, 0u, 0u, 0u};
     if (act & (1u << p)) {
       const uint32_t dst = ((uint32_t(k) - 1u - j) & 1u) ? 2u : 1u;
-      e = PassPlan{1u, j == 0 ? 0u : prev, dst, j & 1u};
+      e = PassPlan{1u, j == 0 ? 0u : prev, dst, j & 1u,
+                   (j == 0 ? CONV_IN : 0u) | (j + 1 == uint32_t(k) ? CONV_OUT : 0u)};
       prev = dst;
       ++j;
     }
@@ -596,7 +623,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
               const Val *__restrict__ vals_in, Val *__restrict__ vals_out, size_t n,
               uint32_t num_tiles, const uint32_t *__restrict__ pass_bins,
               LookbackBuf<Desc> lbuf, LookbackBuf<Desc> lbuf_next, uint32_t nx, uint32_t bit,
-              uint32_t mask) {
+              uint32_t mask, uint32_t conv) {
   constexpr bool PAIRS = !std::is_same<Val, NoValue>::value;
   constexpr int WAVES = THREADS / 64;
   constexpr int TILE = THREADS * ITEMS;
@@ -663,6 +690,12 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   // measurably faster than the per-item waits the compiler would interleave
   // with the counting atomics.
   wait_vmcnt<PAIRS ? ITEMS : 0>();
+  // Raw input (the sort's first pass): to the order-preserving image, which
+  // the tile keeps (a no-op for unsigned ascending keys).
+  if (conv & CONV_IN) {
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) key[j] = Ops::image(key[j]);
+  }
 
   // Per-wave digit counts. Lanes of one LDS atomic that hit the same counter
   // are served one after another, so an item whose digit is the same in all
@@ -672,7 +705,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) {
     const uint32_t d =
-        uint32_t(j) * 64 + lane < wave_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
+        uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
     if (wave_uniform(d)) {
       if (lane == 0)
         __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -753,7 +786,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
       for (int b = 0; b < MB && j0 + b < ITEMS; ++b) {
         const int j = j0 + b;
         const uint32_t d =
-            uint32_t(j) * 64 + lane < wave_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
+            uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
         const uint64_t m = peer_lanes(d, dbits);
         const uint32_t below = popc_below(m);
         peer[b] = lowest_lane(m) | (below << 8);
@@ -785,7 +818,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
       const uint32_t d =
-          uint32_t(j) * 64 + lane < wave_valid ? Ops::digit(key[j], bit, mask) : DUMMY;
+          uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
       if (wave_uniform(d)) {
         uniform |= uint64_t(1) << j;
         pos[j] = lane == 0 ? __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED,
@@ -842,7 +875,13 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
       kk[b] = stage_keys[uint32_t(k0 + b) * THREADS + tid];
 #pragma unroll
     for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b)
-      off[b] = digit_off[Ops::digit(kk[b], bit, mask)];
+      off[b] = digit_off[Ops::image_digit(kk[b], bit, mask)];
+    // The sort's last pass stores raw keys (a wave-uniform branch: the other
+    // passes store the images as they are).
+    if (conv & CONV_OUT) {
+#pragma unroll
+      for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b) kk[b] = Ops::raw(kk[b]);
+    }
 #pragma unroll
     for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b) {
       const uint32_t i = uint32_t(k0 + b) * THREADS + tid;
@@ -881,10 +920,10 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
                 const Val *__restrict__ vals_in, Val *__restrict__ vals_out, size_t n,
                 uint32_t num_tiles, const uint32_t *__restrict__ pass_bins,
                 LookbackBuf<Desc> lbuf, LookbackBuf<Desc> lbuf_next, uint32_t nx, uint32_t bit,
-                uint32_t mask) {
+                uint32_t mask, uint32_t conv) {
   onesweep_tile<Bits, Val, Ops, ITEMS, Desc, THREADS, RANK>(keys_in, keys_out, vals_in, vals_out,
                                                             n, num_tiles, pass_bins, lbuf,
-                                                            lbuf_next, nx, bit, mask);
+                                                            lbuf_next, nx, bit, mask, conv);
 }
 
 // Input, output and scratch buffers of a planned sort (PassPlan numbering).
@@ -912,7 +951,8 @@ planned_onesweep_kernel(PlanBuffers<Bits, Val> b, size_t n, uint32_t num_tiles,
   Val *vout = pl.dst == 1 ? b.vout : b.vscratch;
   onesweep_tile<Bits, Val, Ops, ITEMS, Desc, THREADS, RANK>(kin, kout, vin, vout, n, num_tiles,
                                                             pass_bins, pl.lb ? lb1 : lb0,
-                                                            pl.lb ? lb0 : lb1, nx, bit, mask);
+                                                            pl.lb ? lb0 : lb1, nx, bit, mask,
+                                                            pl.conv);
 }
 
 // ---------------------------------------------------------------------------
@@ -1162,7 +1202,7 @@ rccl_hip_status launch_onesweeps(SortArgs &a, const Layout &l, uint32_t passes,
             static_cast<uint32_t>(l.tiles), bins + size_t(p) * BINS, lb[p & 1],
             p + 1 < passes ? lb[(p + 1) & 1]
                            : LookbackBuf<Desc>{nullptr, nullptr, nullptr, nullptr},
-            nx, bit, mask);
+            nx, bit, mask, (p == 0 ? CONV_IN : 0u) | (p + 1 == passes ? CONV_OUT : 0u));
     RCCL_HIP_TRY(check_launch("radix onesweep"));
     a.cur = out;
   }

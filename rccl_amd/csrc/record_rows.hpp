@@ -59,6 +59,14 @@ struct RowDigits {
   __device__ static __forceinline__ uint32_t digit(const Row<N> &r, uint32_t bit, uint32_t mask) {
     return (word(r, bit >> 5) >> (bit & 31u)) & mask;
   }
+  // Rows are their own order-preserving image (the onesweep's conversions are
+  // no-ops).
+  __device__ static __forceinline__ Row<N> image(const Row<N> &r) { return r; }
+  __device__ static __forceinline__ Row<N> raw(const Row<N> &r) { return r; }
+  __device__ static __forceinline__ uint32_t image_digit(const Row<N> &r, uint32_t bit,
+                                                         uint32_t mask) {
+    return digit(r, bit, mask);
+  }
 };
 
 } // namespace record_sort
