@@ -104,15 +104,15 @@ __device__ __forceinline__ K arith_at(const Arith<K> &r, size_t i) {
 // `before` up to some index and not after it), found from hi downward with
 // doubling steps: O(log(hi - x)) probes, so a short run of equal keys at the
 // end of the range costs a few probes instead of a full binary search.
-template <class R, class Pred>
-__device__ __forceinline__ size_t gallop_down(R r, size_t lo, size_t hi, Pred before) {
-  size_t b = hi, step = 1;  // every x in [b, hi) is not `before`
+template <class I, class R, class Pred>
+__device__ __forceinline__ I gallop_down(R r, I lo, I hi, Pred before) {
+  I b = hi, step = 1;  // every x in [b, hi) is not `before`
   while (b > lo) {
-    const size_t p = b - lo > step ? b - step : lo;
+    const I p = b - lo > step ? b - step : lo;
     if (before(r(p))) {  // the answer is in (p, b]
-      size_t l = p + 1, h = b;
+      I l = p + 1, h = b;
       while (l < h) {
-        const size_t m = l + (h - l) / 2;
+        const I m = l + (h - l) / 2;
         if (before(r(m))) l = m + 1; else h = m;
       }
       return l;
@@ -126,15 +126,15 @@ __device__ __forceinline__ size_t gallop_down(R r, size_t lo, size_t hi, Pred be
 // First index x in [lo, hi) whose item is `after` (the items are not `after`
 // up to some index and are after it), found from lo upward with doubling
 // steps; hi if there is none.
-template <class R, class Pred>
-__device__ __forceinline__ size_t gallop_up(R r, size_t lo, size_t hi, Pred after) {
-  size_t a = lo, step = 1;  // no x in [lo, a) is `after`
+template <class I, class R, class Pred>
+__device__ __forceinline__ I gallop_up(R r, I lo, I hi, Pred after) {
+  I a = lo, step = 1;  // no x in [lo, a) is `after`
   while (a < hi) {
-    const size_t p = hi - a > step ? a + step - 1 : hi - 1;
+    const I p = hi - a > step ? a + step - 1 : hi - 1;
     if (after(r(p))) {  // the answer is in [a, p]
-      size_t l = a, h = p;
+      I l = a, h = p;
       while (l < h) {
-        const size_t m = l + (h - l) / 2;
+        const I m = l + (h - l) / 2;
         if (after(r(m))) h = m; else l = m + 1;
       }
       return l;
@@ -155,12 +155,11 @@ __device__ __forceinline__ size_t gallop_up(R r, size_t lo, size_t hi, Pred afte
 // probe is a dependent round trip: 60 -> 36 us per C5 operation; the tile
 // kernel in LDS, RCCL_SET_TILE_GALLOP); otherwise by binary search.
 // balanced_path_at starts from the merge-path split i of the diagonal.
-template <bool GALLOP, class K, class Cmp, class RA, class RB>
-__device__ __forceinline__ void balanced_path_at(RA a, size_t na, RB b, size_t nb, size_t diag,
-                                                 size_t i, Cmp less, size_t &out_i,
-                                                 size_t &out_j) {
-  const size_t j = diag - i;
-  size_t star = 0;
+template <bool GALLOP, class K, class I = size_t, class Cmp, class RA, class RB>
+__device__ __forceinline__ void balanced_path_at(RA a, I na, RB b, I nb, I diag, I i,
+                                                 Cmp less, I &out_i, I &out_j) {
+  const I j = diag - i;
+  I star = 0;
   // No A item before the split and no B item before it is equal to B[j]:
   // the balanced path is the merge path (the searches below would find
   // i_start = i, j_start = j and move nothing).
@@ -170,36 +169,36 @@ __device__ __forceinline__ void balanced_path_at(RA a, size_t na, RB b, size_t n
     const K key = b(j);
     const auto before_key = [&](const K &x) { return less(x, key); };
     const auto after_key = [&](const K &x) { return less(key, x); };
-    auto lower = [&](auto r, size_t lo, size_t hi) {  // first in [lo, hi) not before key
-      if constexpr (GALLOP) return gallop_down(r, lo, hi, before_key);
+    auto lower = [&](auto r, I lo, I hi) {  // first in [lo, hi) not before key
+      if constexpr (GALLOP) return gallop_down<I>(r, lo, hi, before_key);
       while (lo < hi) {
-        const size_t mid = lo + (hi - lo) / 2;
+        const I mid = lo + (hi - lo) / 2;
         if (before_key(r(mid))) lo = mid + 1; else hi = mid;
       }
       return lo;
     };
-    const size_t i_start = lower(a, 0, i);
-    const size_t j_start = lower(b, 0, j);
-    const size_t a_run = i - i_start;
-    const size_t b_seen = j - j_start;
-    const size_t total = a_run + b_seen;
-    size_t b_adv = std::max(total >> 1, b_seen);
-    const size_t b_end = std::min(nb, j_start + b_adv + 1);
+    const I i_start = lower(a, 0, i);
+    const I j_start = lower(b, 0, j);
+    const I a_run = i - i_start;
+    const I b_seen = j - j_start;
+    const I total = a_run + b_seen;
+    I b_adv = std::max(total >> 1, b_seen);
+    const I b_end = std::min(nb, j_start + b_adv + 1);
     // End of the key's B run within [j, b_end).
-    size_t run_end;
+    I run_end;
     if constexpr (GALLOP) {
-      run_end = gallop_up(b, j, b_end, after_key);
+      run_end = gallop_up<I>(b, j, b_end, after_key);
     } else {
-      size_t lo = j, hi = b_end;
+      I lo = j, hi = b_end;
       while (lo < hi) {
-        const size_t mid = lo + (hi - lo) / 2;
+        const I mid = lo + (hi - lo) / 2;
         if (!after_key(b(mid))) lo = mid + 1; else hi = mid;
       }
       run_end = lo;
     }
-    const size_t b_run = run_end - j_start;
+    const I b_run = run_end - j_start;
     b_adv = std::min(b_adv, b_run);
-    const size_t a_adv = total - b_adv;
+    const I a_adv = total - b_adv;
     star = (a_adv == b_adv + 1 && b_adv < b_run) ? 1 : 0;
     i = i_start + a_adv;
   }
@@ -406,14 +405,17 @@ tile_kernel(const K *__restrict__ a, const V *__restrict__ av, const K *__restri
     {
       const K *ka = sm.keys;
       const K *kb = sm.keys + la;
-      size_t si, sj;
+      // 32-bit indices: the tile is in LDS.
+      uint32_t si, sj;
       const uint32_t diag = min(tid * uint32_t(ITEMS), len);
-      balanced_path<RCCL_SET_TILE_GALLOP, K>([&](size_t x) { return ka[x]; }, la,
-                              [&](size_t x) { return kb[x]; }, lb, diag, less, si, sj);
+      const uint32_t ip = ordering::merge_path_lds<K>(ka, la, kb, lb, diag, less);
+      balanced_path_at<RCCL_SET_TILE_GALLOP, K, uint32_t>(
+          [&](uint32_t x) { return ka[x]; }, la, [&](uint32_t x) { return kb[x]; }, lb, diag,
+          ip, less, si, sj);
       // Every split lies inside the tile; the star of a diagonal past the end
       // is clamped.
-      sm.split_a[tid] = static_cast<uint32_t>(min<size_t>(si, la));
-      sm.split_b[tid] = static_cast<uint32_t>(min<size_t>(sj, lb));
+      sm.split_a[tid] = min(si, la);
+      sm.split_b[tid] = min(sj, lb);
       if (tid == 0) {
         sm.split_a[THREADS] = la;
         sm.split_b[THREADS] = lb;
