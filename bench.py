@@ -686,7 +686,33 @@ def run_c1_latency(torch, np, cub, abi, DeviceBuffer, wd, steps, warmup):
     }
 
 
-LEGS = ("metric", "pairs", "c1", "c2_uniform", "c2_low_entropy", "c3", "merge", "merge_sort",
+def run_reference_size(torch, np, cub, abi, DeviceBuffer, workloads, steps, warmup):
+    """The workload of the reference's one published absolute radix figure: 2^24 u32 keys
+    from its benchmark's xorshift fill (benchmarks/ordering-reference.cu:23-33), sorted
+    ascending; 0.616 ms, 27.2 Gkeys/s on an SM89 GPU
+    (reviews/current-implemented-performance.md:7,193-206). The 64 MiB keys and their
+    scratch fit the MI355X's 256 MB last-level cache, so this is not an HBM-bound figure."""
+    n = 1 << 24
+    keys_t = torch.from_numpy(workloads.reference_bench_u32(n).view(np.int32)).to("cuda")
+    r = run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, None, steps, warmup)
+    del keys_t
+    value = n / (r["ms"] * 1e-3) / 1e9
+    return {
+        "workload": "DeviceRadixSort keys-only, 2^24 u32 keys from the reference benchmark's "
+                    "xorshift fill, ascending, in place (cache-resident working set)",
+        "value": round(value, 3), "unit": "Gkeys/s",
+        "ms_per_step": round(r["ms"], 4), "ms_per_step_min": round(r["ms_min"], 4),
+        "kernel_ms": _rounded(r["kernel_ms"]), "launches": r["launches"],
+        "reference_published": {
+            "value": 27.2, "unit": "Gkeys/s", "ms_per_step": 0.616,
+            "hardware": "an NVIDIA SM89 GPU, not an MI355X",
+            "source": "reviews/current-implemented-performance.md:7,193-206"},
+        "ratio_to_reference_published": round(value / 27.2, 2),
+        "validated": r["validated"],
+    }
+
+
+LEGS = ("metric", "pairs", "reference_size", "c1", "c2_uniform", "c2_low_entropy", "c3", "merge", "merge_sort",
         "set_ops", "record_sort", "compaction", "lower_bound", "cpu_baseline")
 
 
@@ -700,7 +726,7 @@ def main():
                     help="comma-separated legs to run (default: all): " + ", ".join(LEGS))
     ap.add_argument("--no-pairs", action="store_true", help="skip the u64+u32 pairs leg")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip the C1, C2 (uniform, low-entropy) and C3 legs")
+                    help="skip the reference-size, C1, C2 (uniform, low-entropy) and C3 legs")
     ap.add_argument("--no-ordering", action="store_true",
                     help="skip the C4 merge / merge sort, C5 set operation, record sort, "
                          "compaction and lower_bound legs")
@@ -726,7 +752,7 @@ def main():
     if args.no_pairs:
         skip.add("pairs")
     if args.no_configs:
-        skip.update(("c1", "c2_uniform", "c2_low_entropy", "c3"))
+        skip.update(("reference_size", "c1", "c2_uniform", "c2_low_entropy", "c3"))
     if args.no_ordering:
         skip.update(("merge", "merge_sort", "set_ops", "record_sort", "compaction",
                      "lower_bound"))
@@ -804,6 +830,12 @@ def main():
             "radix_onesweep (one pass: 12n read + 12n write)", "radix_onesweep_pairs",
             args.log2n, "u64 keys + u32 values")
         valid = valid and rp["validated"]
+    if "reference_size" in legs:
+        _log("reference benchmark size (2^24 u32)")
+        out["reference_size"] = run_reference_size(torch, np, cub, abi, DeviceBuffer, workloads,
+                                                   args.steps, args.warmup)
+        valid = valid and out["reference_size"]["validated"]
+        _log(f"reference size: {out['reference_size']['ms_per_step']:.3f} ms")
     torch.cuda.empty_cache()
     configs = {}
     log26 = max(args.log2n - 2, 1)

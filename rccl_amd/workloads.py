@@ -230,3 +230,18 @@ def record_rows(arity: int, n: int) -> np.ndarray:
 
 
 RECORD_SORT_ROWS = (1 << 20) + 13  # record_sort_benchmark.rs:4
+
+
+REFERENCE_BENCH_SEED = 0x534D4152545F534F
+
+
+def reference_bench_u32(n: int = 1 << 24) -> np.ndarray:
+    """Keys of the reference's radix-sort benchmark (benchmarks/ordering-reference.cu:23-33,
+    the input of its published 2^24 u32 figure): x = i ^ 0x534d4152545f534f, then the
+    xorshift steps x ^= x << 13, x ^= x >> 7, x ^= x << 17 in 64-bit arithmetic, and the
+    key is the low 32 bits of x."""
+    x = np.arange(n, dtype=np.uint64) ^ _U64(REFERENCE_BENCH_SEED)
+    x ^= x << _U64(13)
+    x ^= x >> _U64(7)
+    x ^= x << _U64(17)
+    return x.astype(np.uint32)

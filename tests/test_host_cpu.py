@@ -402,6 +402,25 @@ def test_workloads_deterministic_and_shaped():
     assert int((bits == 0x7FC00000).sum()) == counts["nan"]
 
 
+def test_reference_bench_keys():
+    """The reference benchmark's xorshift fill (benchmarks/ordering-reference.cu:23-33) in
+    Python integers masked to 64 bits: this checks numpy's wrapping left shifts, the logical
+    right shift and the truncation to the low 32 bits."""
+    def fill(i):
+        m = (1 << 64) - 1
+        x = i ^ workloads.REFERENCE_BENCH_SEED
+        x ^= (x << 13) & m
+        x ^= x >> 7
+        x ^= (x << 17) & m
+        return x & 0xFFFFFFFF
+    k = workloads.reference_bench_u32(1 << 16)
+    assert k.dtype == np.uint32 and k.size == 1 << 16
+    for i in (0, 1, 2, 255, 256, 12345, (1 << 16) - 1):
+        assert int(k[i]) == fill(i), i
+    # The keys use the whole 32-bit range and barely repeat.
+    assert int(k.max()) >= 1 << 31 and np.unique(k).size > (1 << 16) - 16
+
+
 def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=600)
