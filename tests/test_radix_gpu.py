@@ -85,6 +85,17 @@ def test_c1_u32_2pow20(launch):
     np.testing.assert_array_equal(got, oracle.radix_sort("u32", host))
 
 
+@pytest.mark.parametrize("log2n", [20, 24])
+def test_reference_benchmark_input(launch, log2n):
+    """The reference benchmark's xorshift keys (benchmarks/ordering-reference.cu:23-33), at
+    2^20 and at its published size 2^24, against the oracle and numpy's sort."""
+    host = workloads.reference_bench_u32(1 << log2n)
+    got = _sort_keys(launch, host)
+    np.testing.assert_array_equal(got, np.sort(host))
+    if log2n == 20:
+        np.testing.assert_array_equal(got, oracle.radix_sort("u32", host))
+
+
 def test_signed_descending_literal(launch):
     # device_radix_sort_keys_probe.rs:75-97
     got = _sort_keys(launch, np.array([0, -1, -2**31, 7, -9, 2**31 - 1, -1, 0], np.int32), True)
