@@ -56,6 +56,8 @@ Layout layout(size_t key_bytes, size_t value_bytes, size_t n, bool planned) {
   size_t off = 0;
   l.bins = off;
   off += align_up(max_passes * BINS * sizeof(uint32_t), 256);
+  l.skew = off;
+  off += align_up(max_passes * sizeof(uint32_t), 256);
   l.groups = (l.tiles + GROUP - 1) / GROUP;
   l.lb_ginc = align_up(l.tiles * BINS * l.desc_bytes, 256);
   l.lb_gagg = l.lb_ginc + align_up(l.groups * BINS * l.desc_bytes, 256);

@@ -356,6 +356,12 @@ struct PassPlan {
   uint32_t active, src, dst, lb, conv;  // conv: CONV_IN on the first active pass, CONV_OUT on the last
 };
 
+// Skew word of a pass (bins_scan_kernel): 1 when the pass's most frequent
+// digit holds at least 1 / RCCL_RADIX_HOT_DIV of the keys, else 0.
+#ifndef RCCL_RADIX_HOT_DIV
+#define RCCL_RADIX_HOT_DIV 16
+#endif
+
 // Plan flags: some stream (keys or values) is sorted in place (input ==
 // output), and some stream is not (its output must be written even when no
 // pass moves anything).
@@ -411,13 +417,26 @@ __device__ inline void assign_plan(int P, uint32_t trivial, uint32_t flags,
 namespace {
 __global__ void __launch_bounds__(BINS)
 bins_scan_kernel(uint32_t *bins, uint32_t passes, uint32_t n, PassPlan *plan,
-                 uint32_t plan_flags) {
+                 uint32_t plan_flags, uint32_t *skew) {
   __shared__ uint32_t s_wave[BINS / 64];
+  __shared__ uint32_t s_top[BINS / 64];
   __shared__ uint32_t s_trivial;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   if (tid == 0) s_trivial = 0;
   __syncthreads();
+  // Largest digit count of the pass.
+  auto block_max = [&](uint32_t v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, o, 64)));
+    if (lane == 0) s_top[tid >> 6] = v;
+    __syncthreads();
+    uint32_t m = s_top[0];
+#pragma unroll
+    for (int w = 1; w < BINS / 64; ++w) m = max(m, s_top[w]);
+    __syncthreads();
+    return uint64_t(m);
+  };
   for (uint32_t p = 0; p < passes; ++p) {
     const uint32_t c = bins[p * BINS + tid];
     if (plan && c == n) atomicOr(&s_trivial, 1u << p);
@@ -428,6 +447,10 @@ bins_scan_kernel(uint32_t *bins, uint32_t passes, uint32_t n, PassPlan *plan,
     for (uint32_t w = 0; w < (tid >> 6); ++w) excl += s_wave[w];
     bins[p * BINS + tid] = excl;
     __syncthreads();
+    if (skew) {
+      const uint64_t top = block_max(c);
+      if (tid == 0) skew[p] = top * RCCL_RADIX_HOT_DIV >= uint64_t(n) ? 1u : 0u;
+    }
   }
   if (plan && tid == 0) assign_plan(static_cast<int>(passes), s_trivial, plan_flags, plan);
 }
@@ -464,6 +487,26 @@ enum class Rank : int { LaneAtomic = 0, MatchAny = 1 };
 #ifndef RCCL_RADIX_MATCH_BATCH
 #define RCCL_RADIX_MATCH_BATCH 8
 #endif
+// Skewed passes (lane-ordered ranking only): 1 takes each key's rank from
+// the counting atomic (see onesweep_tile), 0 ranks them like uniform passes.
+#ifndef RCCL_RADIX_SKEW_RANKING
+#define RCCL_RADIX_SKEW_RANKING 1
+#endif
+// Items per batch of counter reads in the skewed ranking.
+#ifndef RCCL_RADIX_RANK_BATCH
+#define RCCL_RADIX_RANK_BATCH 8
+#endif
+
+// Tile shapes with the skewed ranking: not those whose keys and values alone
+// take more than 48 registers per thread (u32 keys + 4-byte values at 28
+// items, 8-byte keys + 8-byte values). Their onesweep already fills the
+// register budget, and the skewed branch would make it spill.
+template <class Bits, class Val, int ITEMS>
+constexpr bool skew_ranking() {
+  constexpr size_t VREGS = std::is_same<Val, NoValue>::value ? 0 : (sizeof(Val) + 3) / 4;
+  return RCCL_RADIX_SKEW_RANKING &&
+         size_t(ITEMS) * ((sizeof(Bits) + 3) / 4 + VREGS) <= 48;
+}
 
 // s_waitcnt vmcnt(N): wait until at most N vector memory operations of this
 // wave are outstanding (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt
@@ -622,8 +665,9 @@ __device__ __forceinline__ void
 onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
               const Val *__restrict__ vals_in, Val *__restrict__ vals_out, size_t n,
               uint32_t num_tiles, const uint32_t *__restrict__ pass_bins,
-              LookbackBuf<Desc> lbuf, LookbackBuf<Desc> lbuf_next, uint32_t nx, uint32_t bit,
-              uint32_t mask, uint32_t conv) {
+              const uint32_t *__restrict__ pass_skew, LookbackBuf<Desc> lbuf,
+              LookbackBuf<Desc> lbuf_next, uint32_t nx, uint32_t bit, uint32_t mask,
+              uint32_t conv) {
   constexpr bool PAIRS = !std::is_same<Val, NoValue>::value;
   constexpr int WAVES = THREADS / 64;
   constexpr int TILE = THREADS * ITEMS;
@@ -701,16 +745,53 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   // are served one after another, so an item whose digit is the same in all
   // 64 lanes (skewed or presorted keys, a constant byte) is counted by one
   // lane adding 64.
+  //
+  // Skewed passes (bins_scan_kernel flags a pass whose most frequent digit
+  // holds at least 1 / RCCL_RADIX_HOT_DIV of the keys; lane-ordered ranking
+  // only) count with returning atomics, whose results are the keys' ranks
+  // within their wave and digit. Each thread parks its ranks in its own slots
+  // of the staging area (free until the keys are staged) and reads them back
+  // after the count, so the ranking below reads each wave's digit start
+  // instead of adding to it: a read that many lanes share is served once,
+  // where an atomic on a hot digit's counter is served lane by lane.
   uint32_t *wcnt = cnt[wave];
+  constexpr bool SKEW_PATH = RANK == Rank::LaneAtomic && skew_ranking<Bits, Val, ITEMS>();
+  const bool skewed = SKEW_PATH && pass_skew && *pass_skew != 0;
+  uint32_t *rank_slot = reinterpret_cast<uint32_t *>(stage_raw) + wave * WAVE_ITEMS + lane;
+  uint32_t pos[ITEMS];
+  if (skewed) {
+    uint32_t ret[ITEMS];
+    uint64_t uniform = 0;
 #pragma unroll
-  for (int j = 0; j < ITEMS; ++j) {
-    const uint32_t d =
-        uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
-    if (wave_uniform(d)) {
-      if (lane == 0)
-        __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    } else {
-      __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (int j = 0; j < ITEMS; ++j) {
+      const uint32_t d =
+          uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
+      if (wave_uniform(d)) {
+        uniform |= uint64_t(1) << j;
+        ret[j] = lane == 0 ? __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_WORKGROUP)
+                           : 0u;
+      } else {
+        ret[j] =
+            __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      if (uniform & (uint64_t(1) << j)) ret[j] = __builtin_amdgcn_readfirstlane(ret[j]) + lane;
+      rank_slot[j * 64] = ret[j];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      const uint32_t d =
+          uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
+      if (wave_uniform(d)) {
+        if (lane == 0)
+          __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      } else {
+        __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
     }
   }
   lds_barrier();
@@ -721,16 +802,12 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   const uint32_t group = tile / GROUP;
   const int gfirst = static_cast<int>(group) * GROUP;
   uint32_t count = 0, tile_inc = 0;
-  uint32_t wc[WAVES];
   Desc lb[lookback_window<Desc>()];
   Desc gi[GWIN];
   uint32_t ga[GWIN];
   if (tid < BINS) {
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) {
-      wc[w] = cnt[w][tid];
-      count += wc[w];
-    }
+    for (int w = 0; w < WAVES; ++w) count += cnt[w][tid];
     store_agent(&lbuf.tile[size_t(tile) * BINS + tid],
                 static_cast<Desc>((tile == 0 ? DI::INCL : DI::AGG) | Desc(count)));
     add_agent(&lbuf.gagg[size_t(group) * BINS + tid], (1u << GAGG_SHIFT) | count);
@@ -755,12 +832,13 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     tile_start = tile_inc - count;
     for (uint32_t w = 0; w < wave; ++w) tile_start += wave_sum[w];
     // Each wave's counter becomes the tile position of its first key of this
-    // digit.
+    // digit (the counts are read again rather than held in registers).
     uint32_t run = tile_start;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) {
+      const uint32_t c = cnt[w][tid];
       cnt[w][tid] = run;
-      run += wc[w];
+      run += c;
     }
   }
   if (tid < WAVES) cnt[tid][DUMMY] = TILE;
@@ -772,7 +850,6 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   // lane) order, which is source order; dummies all land in the spare slot.
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j) launder(key[j]);
-  uint32_t pos[ITEMS];
   if constexpr (RANK == Rank::MatchAny) {
     // Match-any, in batches of MB items (each item's peer data is held until
     // its base returns); a batch's atomics are issued together. Digits can
@@ -803,6 +880,32 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
         const uint32_t base = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(
             static_cast<int>((peer[b] & 63u) << 2), static_cast<int>(pos[j])));
         pos[j] = min(base + (peer[b] >> 8), uint32_t(TILE));
+        stage_keys[pos[j]] = key[j];
+      }
+    }
+  } else if (skewed) {
+    // Position = the wave's start for the digit + the rank from the count.
+    // Every thread reads its parked ranks before any key is staged over them.
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) pos[j] = rank_slot[j * 64];
+    lds_barrier();
+    // In batches: a batch's counter reads are issued together, then its keys
+    // staged (all at once would hold a second register per key).
+    constexpr int RB = RCCL_RADIX_RANK_BATCH;
+#pragma unroll
+    for (int j0 = 0; j0 < ITEMS; j0 += RB) {
+      uint32_t start[RB];
+#pragma unroll
+      for (int j = j0; j < j0 + RB && j < ITEMS; ++j) {
+        const uint32_t d =
+            uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
+        start[j - j0] = wcnt[d];
+      }
+#pragma unroll
+      for (int j = j0; j < j0 + RB && j < ITEMS; ++j) asm volatile("" : "+v"(start[j - j0]));
+#pragma unroll
+      for (int j = j0; j < j0 + RB && j < ITEMS; ++j) {
+        pos[j] = min(pos[j] + start[j - j0], uint32_t(TILE));
         stage_keys[pos[j]] = key[j];
       }
     }
@@ -919,11 +1022,12 @@ __global__ void __launch_bounds__(THREADS, RCCL_RADIX_WAVES_PER_SIMD)
 onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
                 const Val *__restrict__ vals_in, Val *__restrict__ vals_out, size_t n,
                 uint32_t num_tiles, const uint32_t *__restrict__ pass_bins,
-                LookbackBuf<Desc> lbuf, LookbackBuf<Desc> lbuf_next, uint32_t nx, uint32_t bit,
-                uint32_t mask, uint32_t conv) {
+                const uint32_t *__restrict__ pass_skew, LookbackBuf<Desc> lbuf,
+                LookbackBuf<Desc> lbuf_next, uint32_t nx, uint32_t bit, uint32_t mask,
+                uint32_t conv) {
   onesweep_tile<Bits, Val, Ops, ITEMS, Desc, THREADS, RANK>(keys_in, keys_out, vals_in, vals_out,
-                                                            n, num_tiles, pass_bins, lbuf,
-                                                            lbuf_next, nx, bit, mask, conv);
+                                                            n, num_tiles, pass_bins, pass_skew,
+                                                            lbuf, lbuf_next, nx, bit, mask, conv);
 }
 
 // Input, output and scratch buffers of a planned sort (PassPlan numbering).
@@ -940,7 +1044,8 @@ struct PlanBuffers {
 template <class Bits, class Val, class Ops, int ITEMS, class Desc, int THREADS, Rank RANK>
 __global__ void __launch_bounds__(THREADS, RCCL_RADIX_WAVES_PER_SIMD)
 planned_onesweep_kernel(PlanBuffers<Bits, Val> b, size_t n, uint32_t num_tiles,
-                        const uint32_t *__restrict__ pass_bins, const PassPlan *__restrict__ plan,
+                        const uint32_t *__restrict__ pass_bins,
+                        const uint32_t *__restrict__ pass_skew, const PassPlan *__restrict__ plan,
                         LookbackBuf<Desc> lb0, LookbackBuf<Desc> lb1, uint32_t nx, uint32_t bit,
                         uint32_t mask) {
   const PassPlan pl = *plan;
@@ -950,7 +1055,7 @@ planned_onesweep_kernel(PlanBuffers<Bits, Val> b, size_t n, uint32_t num_tiles,
   const Val *vin = pl.src == 0 ? b.vin : (pl.src == 1 ? b.vout : b.vscratch);
   Val *vout = pl.dst == 1 ? b.vout : b.vscratch;
   onesweep_tile<Bits, Val, Ops, ITEMS, Desc, THREADS, RANK>(kin, kout, vin, vout, n, num_tiles,
-                                                            pass_bins, pl.lb ? lb1 : lb0,
+                                                            pass_bins, pass_skew, pl.lb ? lb1 : lb0,
                                                             pl.lb ? lb0 : lb1, nx, bit, mask,
                                                             pl.conv);
 }
@@ -1084,6 +1189,7 @@ struct Layout {
   size_t desc_bytes = 4;
   bool small = false;  // small_tiles()
   size_t bins = 0;
+  size_t skew = 0;  // one skew word per pass (bins_scan_kernel)
   // Look-back buffers: tile descriptors, group prefixes, group aggregates and
   // the pass's tile tickets.
   size_t lb[2] = {0, 0};
@@ -1150,7 +1256,8 @@ void lookback_buffers(const SortArgs &a, const Layout &l, LookbackBuf<Desc> (&lb
 template <class Bits, class Val, class Ops, class Desc, Rank RANK, int THREADS, int ITEMS,
           bool PLANNED>
 rccl_hip_status launch_onesweeps(SortArgs &a, const Layout &l, uint32_t passes,
-                                 const uint32_t *bins, const PassPlan *plan, uint32_t nx) {
+                                 const uint32_t *bins, const uint32_t *skew, const PassPlan *plan,
+                                 uint32_t nx) {
   LookbackBuf<Desc> lb[2];
   lookback_buffers(a, l, lb);
   size_t resident = 0;
@@ -1179,8 +1286,8 @@ rccl_hip_status launch_onesweeps(SortArgs &a, const Layout &l, uint32_t passes,
       KernelTimer t("radix_onesweep", a.stream, a.n);
       planned_onesweep_kernel<Bits, Val, Ops, ITEMS, Desc, THREADS, RANK>
           <<<dim3(grid), THREADS, 0, a.stream>>>(b, a.n, static_cast<uint32_t>(l.tiles),
-                                                 bins + size_t(p) * BINS, plan + p, lb[0], lb[1],
-                                                 nx, bit, mask);
+                                                 bins + size_t(p) * BINS, skew + p,
+                                                 plan + p, lb[0], lb[1], nx, bit, mask);
       RCCL_HIP_TRY(check_launch("radix onesweep"));
     }
     a.cur = 0;
@@ -1199,7 +1306,8 @@ rccl_hip_status launch_onesweeps(SortArgs &a, const Layout &l, uint32_t passes,
         <<<dim3(grid), THREADS, 0, a.stream>>>(
             static_cast<const Bits *>(kin), static_cast<Bits *>(a.keys[out]),
             static_cast<const Val *>(vin), static_cast<Val *>(a.vals[out]), a.n,
-            static_cast<uint32_t>(l.tiles), bins + size_t(p) * BINS, lb[p & 1],
+            static_cast<uint32_t>(l.tiles), bins + size_t(p) * BINS, skew + p,
+            lb[p & 1],
             p + 1 < passes ? lb[(p + 1) & 1]
                            : LookbackBuf<Desc>{nullptr, nullptr, nullptr, nullptr},
             nx, bit, mask, (p == 0 ? CONV_IN : 0u) | (p + 1 == passes ? CONV_OUT : 0u));
@@ -1235,6 +1343,7 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
     return caps.rank == Rank::LaneAtomic ? launch_single_tile<Bits, Val, Ops, Rank::LaneAtomic>(a)
                                          : launch_single_tile<Bits, Val, Ops, Rank::MatchAny>(a);
   uint32_t *bins = reinterpret_cast<uint32_t *>(a.ws + l.bins);
+  uint32_t *skew = reinterpret_cast<uint32_t *>(a.ws + l.skew);
   {
     KernelTimer t("radix_init", a.stream, 0);
     init_kernel<<<1, 256, 0, a.stream>>>(bins, passes);
@@ -1268,7 +1377,7 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
   {
     KernelTimer t("radix_bins_scan", a.stream, passes * BINS);
     bins_scan_kernel<<<1, BINS, 0, a.stream>>>(bins, passes, static_cast<uint32_t>(a.n), plan,
-                                                a.plan_flags);
+                                                a.plan_flags, skew);
   }
   RCCL_HIP_TRY(check_launch("radix bins scan"));
   constexpr int ITEMS = items_for(sizeof(Bits), VBYTES);
@@ -1278,23 +1387,23 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
   const bool la = caps.rank == LA;
   if (a.planned)
     return la ? launch_onesweeps<Bits, Val, Ops, Desc, LA, THREADS, ITEMS, true>(
-                    a, l, passes, bins, plan, caps.nx)
+                    a, l, passes, bins, skew, plan, caps.nx)
               : launch_onesweeps<Bits, Val, Ops, Desc, MA, THREADS, ITEMS, true>(
-                    a, l, passes, bins, plan, caps.nx);
+                    a, l, passes, bins, skew, plan, caps.nx);
   // Small tiles serve unplanned sorts only, all below 2^30 items (32-bit
   // descriptors); the layout chose them for this n.
   if constexpr (sizeof(Desc) == 4) {
     if (l.small)
       return la ? launch_onesweeps<Bits, Val, Ops, Desc, LA, SMALL_THREADS, SITEMS, false>(
-                      a, l, passes, bins, plan, caps.nx)
+                      a, l, passes, bins, skew, plan, caps.nx)
                 : launch_onesweeps<Bits, Val, Ops, Desc, MA, SMALL_THREADS, SITEMS, false>(
-                      a, l, passes, bins, plan, caps.nx);
+                      a, l, passes, bins, skew, plan, caps.nx);
   }
   if (l.small) return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix small-tile layout");
   return la ? launch_onesweeps<Bits, Val, Ops, Desc, LA, THREADS, ITEMS, false>(
-                  a, l, passes, bins, plan, caps.nx)
+                  a, l, passes, bins, skew, plan, caps.nx)
             : launch_onesweeps<Bits, Val, Ops, Desc, MA, THREADS, ITEMS, false>(
-                  a, l, passes, bins, plan, caps.nx);
+                  a, l, passes, bins, skew, plan, caps.nx);
 }
 
 template <class Bits, class Ops>

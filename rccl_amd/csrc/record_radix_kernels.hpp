@@ -221,8 +221,8 @@ row_onesweep_kernel(RowBuffers<N, Val> b, size_t n, uint32_t num_tiles,
   const Val *vin = pl.src == 0 ? b.vin : (pl.src == 1 ? b.vout : b.vscratch);
   Val *vout = pl.dst == 1 ? b.vout : b.vscratch;
   radix::onesweep_tile<Row<N>, Val, RowDigits<N>, ITEMS, uint32_t, RADIX_THREADS, RANK>(
-      kin, kout, vin, vout, n, num_tiles, pass_bins, pl.lb ? lb1 : lb0, pl.lb ? lb0 : lb1, nx,
-      bit, 0xFFu, pl.conv);
+      kin, kout, vin, vout, n, num_tiles, pass_bins, nullptr, pl.lb ? lb1 : lb0,
+      pl.lb ? lb0 : lb1, nx, bit, 0xFFu, pl.conv);
 }
 
 // ---------------------------------------------------------------------------

@@ -447,3 +447,54 @@ def test_small_tile_counts(launch, tiles, delta):
             wk, wv = oracle.radix_sort(kind, keys, values)
             np.testing.assert_array_equal(gk, wk)
             np.testing.assert_array_equal(gv, wv)
+
+
+def _skewed_bits(n, nbytes, nhot, seed, runs):
+    """Random keys of `nbytes` bytes where each of `nhot` dictionary values
+    takes about 11% of the positions, so that every byte has up to `nhot`
+    digits above 1/16 of the keys (the onesweep's hot digits; more than four
+    leaves the rest on the counting atomics). With `runs`, blocks of 3,000
+    keys are sorted, so that whole 64-key items share a hot or a cold digit."""
+    raw = workloads.hash_range(seed, n)
+    pick = workloads.hash_range(seed ^ 0x5EED, n)
+    dictionary = workloads.hash_range(seed ^ 0xD1C7, max(nhot, 1))
+    slot = (pick >> np.uint64(40)) % np.uint64(9)  # slots 0..nhot-1 hot
+    hot = slot < np.uint64(nhot)
+    bits = np.where(hot, dictionary[np.minimum(slot, np.uint64(max(nhot, 1) - 1)).astype(np.int64)],
+                    raw)
+    if nbytes == 4:
+        bits = (bits >> np.uint64(32)).astype(np.uint32)
+    if runs:
+        for s in range(0, n, 3000):
+            bits[s:s + 3000].sort()
+    return bits
+
+
+@pytest.mark.parametrize("nhot", [1, 2, 4, 6])
+@pytest.mark.parametrize("runs", [False, True])
+@pytest.mark.parametrize("kind", ["u32", "f32", "u64"])
+@pytest.mark.parametrize("descending", [False, True])
+def test_skewed_digits(launch, nhot, runs, kind, descending):
+    """Passes with up to four hot digits count and rank those digits by
+    ballot instead of LDS atomics; ragged sizes put dummies in the last
+    tile."""
+    dt = np.dtype(oracle.KIND_DTYPES[kind])
+    n = 1_000_003 if nhot % 2 else 3 * 17_408 + 1_234
+    host = _skewed_bits(n, dt.itemsize, nhot, 0x5CE3 + nhot, runs).view(dt)
+    got = _sort_keys(launch, host, descending)
+    want = oracle.radix_sort(kind, host, descending=descending)
+    np.testing.assert_array_equal(_bits(got), _bits(want))
+
+
+@pytest.mark.parametrize("nhot", [1, 3, 5])
+@pytest.mark.parametrize("descending", [False, True])
+def test_skewed_digits_pairs_stable(launch, nhot, descending):
+    """u64 keys with u32 index values (the C2 pair shape): ties among the
+    hot keys must keep their input order."""
+    n = 700_001
+    keys = _skewed_bits(n, 8, nhot, 0xA11 + nhot, False)
+    vals = np.arange(n, dtype=np.uint32)
+    got_k, got_v = _sort_pairs(launch, keys, vals, descending)
+    want_k, want_v = oracle.radix_sort("u64", keys, vals, descending=descending)
+    np.testing.assert_array_equal(got_k, want_k)
+    np.testing.assert_array_equal(got_v, want_v)
