@@ -36,11 +36,14 @@ def _log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _fingerprint(torch, t):
-    """Order-independent fingerprint: wrapping sums of the words and squares."""
-    w = t.to(torch.int64)
-    m = (1 << 64) - 1
-    return int(w.sum().item()) & m, int((w * w).sum().item()) & m
+def _sorted_equal(torch, out, src):
+    """Exact check: `out` equals `src` sorted ascending in unsigned order
+    (torch.sort through a flipped sign bit), word for word; `src` and `out`
+    are int32 or int64 storage of u32 or u64 keys."""
+    sign = torch.tensor(-(1 << (8 * src.element_size() - 1)), dtype=src.dtype,
+                        device=src.device)
+    want = torch.sort(src ^ sign).values ^ sign
+    return bool(torch.equal(out, want))
 
 
 def _nondecreasing(torch, t, bits):
@@ -232,8 +235,7 @@ def run_radix(torch, np, cub, abi, DeviceBuffer, keys_t, values_t, steps, warmup
     elif values_t is not None and not descending and np.dtype(kdt).kind == "u":
         ok = _check_stable_pairs(torch, pristine_k, keys.tensor, values.tensor, bits)
     else:
-        ok = _nondecreasing(torch, keys.tensor, bits) and \
-            _fingerprint(torch, keys.tensor) == _fingerprint(torch, pristine_k)
+        ok = _sorted_equal(torch, keys.tensor, pristine_k)
     return {"n": n, "ms": t["ms"], "ms_mean": t["mean"], "ms_min": t["min"], "ms_wall": t["wall"],
             "kernel_ms": t["kernel_ms"], "launches": t["launches"], "validated": bool(ok)}
 
@@ -254,6 +256,46 @@ def radix_leg(r, n, workload, key_bytes_model, pass_bytes, kernel_desc, traffic_
                              profiled_traffic(traffic_kernel, log2n)),
         "kernel_ms": _rounded(r["kernel_ms"]), "launches": r["launches"],
         "validated": r["validated"],
+    }
+
+
+def run_hbm_reference(torch, n, steps, warmup):
+    """This GPU's measured HBM rates in the same run, beside the 8 TB/s peak:
+    a plain device-to-device copy (torch copy_) and a read (torch sum into
+    one int64) of n u32 words (2^28: 1 GiB), each the median of event-timed
+    steps after warm-up."""
+    src = torch.ones(n, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream()
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        for s, e in ev:
+            s.record(stream)
+            fn()
+            e.record(stream)
+        torch.cuda.synchronize()
+        ms = sorted(s.elapsed_time(e) for s, e in ev)
+        mid = len(ms) // 2
+        return ms[mid] if len(ms) % 2 else 0.5 * (ms[mid - 1] + ms[mid])
+
+    copy_ms = timed(lambda: dst.copy_(src))
+    read_ms = timed(lambda: torch.sum(src, dtype=torch.int64))
+    ok = bool(torch.equal(dst, src)) and int(torch.sum(src, dtype=torch.int64).item()) == n
+    del src, dst
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"torch copy_ and sum of 2^{n.bit_length() - 1} u32 words on this GPU",
+        "copy_ms": round(copy_ms, 4), "read_ms": round(read_ms, 4),
+        "copy_GBps": round(8.0 * n / (copy_ms * 1e-3) / 1e9, 1),
+        "read_GBps": round(4.0 * n / (read_ms * 1e-3) / 1e9, 1),
+        "copy_frac_of_peak": round(8.0 * n / (copy_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "read_frac_of_peak": round(4.0 * n / (read_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "validated": ok,
     }
 
 
@@ -356,9 +398,7 @@ def run_merge(torch, np, cub, abi, DeviceBuffer, wd, log2_each, steps, warmup):
 
     ms, ms_min, wall, kms, launches, _ = _steps(torch, abi, launch.stream(), steps, warmup, step)
     total = 2 * n_each
-    ok = _nondecreasing(torch, out.tensor, 32)
-    ok = ok and _fingerprint(torch, out.tensor) == tuple(
-        (x + y) & ((1 << 64) - 1) for x, y in zip(_fingerprint(torch, a), _fingerprint(torch, b)))
+    ok = _sorted_equal(torch, out.tensor, torch.cat((a, b)))
     # Stability: on equal keys every A payload (high bit clear) precedes B's.
     k64 = out.tensor.to(torch.int64) & 0xFFFFFFFF
     src_b = (outv.tensor < 0)
@@ -394,8 +434,7 @@ def run_merge_sort(torch, np, cub, abi, DeviceBuffer, wd, log2n, steps, warmup):
 
     ms, ms_min, wall, kms, launches, per_step = _steps(torch, abi, launch.stream(), steps,
                                                            warmup, step)
-    ok = _nondecreasing(torch, out.tensor, 32)
-    ok = ok and _fingerprint(torch, out.tensor) == _fingerprint(torch, keys_t)
+    ok = _sorted_equal(torch, out.tensor, keys_t)
     res = {
         "workload": f"C4 DeviceMergeSort keys: 2^{log2n} u32 keys in [0, 2^24), ascending "
                     "(copy form: input left untouched)",
@@ -712,8 +751,9 @@ def run_reference_size(torch, np, cub, abi, DeviceBuffer, workloads, steps, warm
     }
 
 
-LEGS = ("metric", "pairs", "reference_size", "c1", "c2_uniform", "c2_low_entropy", "c3", "merge", "merge_sort",
-        "set_ops", "record_sort", "compaction", "lower_bound", "cpu_baseline")
+LEGS = ("metric", "hbm_reference", "pairs", "reference_size", "c1", "c2_uniform",
+        "c2_low_entropy", "c3", "merge", "merge_sort", "set_ops", "record_sort", "compaction",
+        "lower_bound", "cpu_baseline")
 
 
 def main():
@@ -818,6 +858,22 @@ def main():
             "validated": r32["validated"],
         })
         valid = valid and r32["validated"]
+    if "hbm_reference" in legs:
+        _log("HBM reference: device copy and read")
+        ref = run_hbm_reference(torch, n, args.steps, args.warmup)
+        if "metric" in legs:
+            # The sort, its onesweep pass and its histogram against the rates
+            # this GPU reached for a copy (read + write) and a read.
+            km = out["kernel_ms"]
+            ref["sort_vs_copy"] = round(36.0 * n / (out["ms_per_step"] * 1e-3) / 1e9 /
+                                        ref["copy_GBps"], 4)
+            ref["onesweep_vs_copy"] = round(8.0 * n / (km["radix_onesweep"] * 1e-3) / 1e9 /
+                                            ref["copy_GBps"], 4)
+            ref["histogram_vs_read"] = round(4.0 * n / (km["radix_histogram"] * 1e-3) / 1e9 /
+                                             ref["read_GBps"], 4)
+        out["hbm_reference"] = ref
+        valid = valid and ref["validated"]
+        _log(f"copy {ref['copy_GBps']} GB/s, read {ref['read_GBps']} GB/s")
     if "pairs" in legs:
         pk, pv = wd.metric_pairs(n)
         rp = run_radix(torch, np, cub, abi, DeviceBuffer, pk, pv, args.steps, args.warmup)

@@ -10,14 +10,22 @@
  *
  * Conventions (rccl-cub/src/error.rs:3-25, rccl-thrust/src/cuda.rs):
  *  - All pointers are device pointers unless stated otherwise; sizes are in
- *    elements. The caller owns inputs, outputs and the workspace; no
- *    ordering entry point allocates device memory (only the one-time device
- *    self-check of rccl_hip_program_load allocates and frees 4 bytes).
+ *    elements. The caller owns inputs, outputs and the workspace; no entry
+ *    point allocates device memory (the one-time device probes of
+ *    rccl_hip_program_load write a static device array of the library).
+ *  - The first call on a device probes it (lane order of LDS atomics, block
+ *    placement, CU count) with launches on the null stream and a synchronous
+ *    copy, unless rccl_hip_program_load already did. On a stream under HIP
+ *    graph capture such a first call returns RCCL_HIP_ERROR_INVALID_ARGUMENT
+ *    before any launch: load the program on the device before capturing.
  *  - Work is enqueued on `stream` and is asynchronous (CUB semantics). The
  *    Thrust-style synchronous behaviour is the host layer's job.
  *  - Every call validates all arguments before the first launch and returns a
- *    status that maps 1:1 onto DeviceAlgorithmError. Details of the last
- *    failure on the calling thread are available from rccl_hip_last_error().
+ *    status that maps onto DeviceAlgorithmError, one code per variant (1-8);
+ *    9 is an invalid-argument guard with no variant, and
+ *    InvalidHistogramShape (error.rs:19, DeviceHistogram) has no code, as
+ *    histograms are outside this library. Details of the last failure on
+ *    the calling thread are available from rccl_hip_last_error().
  *  - Empty inputs (and empty radix bit windows) return success without
  *    launching anything.
  */
@@ -230,7 +238,9 @@ RCCL_HIP_API rccl_hip_status rccl_hip_radix_configure(int ranking, int tile_orde
  * exceeds that size returns RCCL_HIP_ERROR_WORKSPACE_TOO_SMALL before any
  * launch. Every call on one device shares that device's array (each call
  * clears what it uses), so calls that overlap on one device (different
- * streams, or threads) race: serialize them. */
+ * streams, or threads) race: serialize them. Under graph capture, load the
+ * program on the device first (rccl_hip_program_load): the device probe of a
+ * first call cannot run on a capturing stream (RCCL_HIP_ERROR_INVALID_ARGUMENT). */
 RCCL_HIP_API rccl_hip_status rccl_hip_radix_sort_static(rccl_hip_key_kind key,
                                                         size_t value_bytes, rccl_hip_order order,
                                                         void *keys, void *values,

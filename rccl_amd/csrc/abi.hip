@@ -113,11 +113,11 @@ rccl_hip_status resident_blocks(const void *kernel, int threads, size_t *blocks)
   return ok();
 }
 
-rccl_hip_status check_xcd_rows(const void *kernel, int threads, uint32_t run, const char *role) {
+rccl_hip_status fit_tile_order(const void *kernel, int threads, uint32_t run, uint32_t *nx) {
+  if (*nx != XCDS) return ok();
   size_t blocks = 0;
   RCCL_HIP_TRY(resident_blocks(kernel, threads, &blocks));
-  if (blocks < 2 * size_t(XCDS) * run)
-    return set_error(RCCL_HIP_ERROR_LAUNCH, role, 2 * XCDS * run, blocks);
+  if (blocks < 2 * size_t(XCDS) * run) *nx = 1;
   return ok();
 }
 

@@ -7,6 +7,7 @@
 #include <cstdint>
 
 #include "rccl_hip.h"
+#include "sizes.hpp"
 
 namespace rccl_hip {
 
@@ -44,7 +45,6 @@ private:
   hipStream_t stream_;
 };
 
-inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // Whether the byte ranges [a, a + an) and [b, b + bn) share a byte (empty or
 // null ranges share none).
@@ -73,21 +73,39 @@ inline bool outputs_overlap_inputs(const ByteRange (&outs)[NO], const ByteRange 
   return false;
 }
 
+// Buffers of a sort with a key stream and an optional value stream (value
+// bytes 0: none), each sorted in place (input == output) or into its own
+// output: whether some output shares a byte with an input it is not the
+// in-place output of, or with the other output. Passes read their input
+// while other blocks already write, so such a call would race.
+inline bool sort_streams_overlap(const void *in_keys, const void *out_keys, size_t key_bytes,
+                                 const void *in_values, const void *out_values,
+                                 size_t value_bytes) {
+  return (in_keys != out_keys && ranges_overlap(out_keys, key_bytes, in_keys, key_bytes)) ||
+         (in_values != out_values &&
+          ranges_overlap(out_values, value_bytes, in_values, value_bytes)) ||
+         ranges_overlap(out_keys, key_bytes, in_values, value_bytes) ||
+         ranges_overlap(out_values, value_bytes, in_keys, key_bytes) ||
+         ranges_overlap(out_keys, key_bytes, out_values, value_bytes);
+}
+
 // Blocks of `kernel` (launched with `threads` threads and no dynamic LDS) that
 // the current device holds at once: CUs x resident blocks per CU. Cached per
 // device and kernel.
 rccl_hip_status resident_blocks(const void *kernel, int threads, size_t *blocks);
 
 // The XCD-ordered look-back (xcd_order_tile) needs two rows of XCD runs
-// resident at once: RCCL_HIP_ERROR_LAUNCH where `kernel` cannot hold them, so
-// that a device too small for it reports an error instead of waiting forever.
-rccl_hip_status check_xcd_rows(const void *kernel, int threads, uint32_t run, const char *role);
+// resident at once. Where `kernel` cannot hold them, *nx becomes 1: its blocks
+// claim tiles from the atomic ticket instead (a tile is claimed only by a
+// started block, so the look-back cannot wait on an unstarted one).
+rccl_hip_status fit_tile_order(const void *kernel, int threads, uint32_t run, uint32_t *nx);
 
 // Tile order for the current device: XCDS where its blocks land on the XCDs
 // round-robin (XCD-ordered tiles), 1 where tiles must be claimed from an
 // atomic ticket (the load-time probe failed, or rccl_hip_radix_configure
-// asked for tickets).
-rccl_hip_status tile_order(uint32_t *nx);
+// asked for tickets). Fails, before any launch, on a stream under graph
+// capture when the device was not probed yet (rccl_hip_program_load probes it).
+rccl_hip_status tile_order(uint32_t *nx, hipStream_t stream);
 
 inline size_t key_bytes(rccl_hip_key_kind k) {
   switch (k) {
@@ -162,7 +180,6 @@ __device__ __forceinline__ T add_agent(T *p, T v) {
 // tile, hence has finished), and the look-back cannot deadlock. The grid is
 // rounded up to whole rows of 8 * RUN blocks (xcd_order_grid); blocks whose
 // tile is past the end return.
-constexpr uint32_t XCDS = 8;
 template <uint32_t RUN>
 __device__ __forceinline__ uint32_t xcd_order_tile(uint32_t block) {
   const uint32_t x = block % XCDS, j = block / XCDS;

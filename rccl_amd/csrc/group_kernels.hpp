@@ -332,11 +332,9 @@ rccl_hip_status run(const GroupArgs &a) {
   uint64_t *desc = reinterpret_cast<uint64_t *>(ws + l.desc);
   const size_t words = lookback::state_words(l.tiles);
   uint32_t nx = 1;
-  RCCL_HIP_TRY(tile_order(&nx));
-  if (nx == XCDS)
-    RCCL_HIP_TRY(check_xcd_rows(
-        reinterpret_cast<const void *>(&group_tile_kernel<K, P, Op, ITEMS>), THREADS, XCD_RUN,
-        "group tile does not fit on the device"));
+  RCCL_HIP_TRY(tile_order(&nx, a.stream));
+  RCCL_HIP_TRY(fit_tile_order(reinterpret_cast<const void *>(&group_tile_kernel<K, P, Op, ITEMS>),
+                              THREADS, XCD_RUN, &nx));
   {
     KernelTimer t("group_clear", a.stream, words);
     group_clear_kernel<<<dim3(static_cast<uint32_t>(std::min<size_t>((words + 255) / 256, 1024))),

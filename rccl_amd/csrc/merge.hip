@@ -169,12 +169,12 @@ rccl_hip_status rccl_hip_merge_sort(rccl_hip_key_kind key, size_t value_bytes, r
   if (value_bytes && (!in_values || !out_values))
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "merge sort values");
   {
-    // Each stream is sorted in place (input == output) or into a disjoint
-    // output; a partly overlapping one would be read and written by one pass.
+    // Each stream is sorted in place (input == output) or into an output
+    // disjoint from both inputs and the other output; anything else would be
+    // read and written by one pass.
     const size_t kb = sat_mul(key_bytes(key), n), vb = sat_mul(value_bytes, n);
-    if ((in_keys != out_keys && ranges_overlap(in_keys, kb, out_keys, kb)) ||
-        (value_bytes && in_values != out_values && ranges_overlap(in_values, vb, out_values, vb)) ||
-        ranges_overlap(out_keys, kb, out_values, vb))
+    if (sort_streams_overlap(in_keys, out_keys, kb, value_bytes ? in_values : nullptr,
+                             value_bytes ? out_values : nullptr, vb))
       return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "merge sort buffers overlap");
   }
   if (lowers_to_radix(key, n))

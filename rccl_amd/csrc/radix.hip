@@ -45,31 +45,6 @@ rccl_hip_status static_workspace(void **out) {
   return ok();
 }
 
-Layout layout(size_t key_bytes, size_t value_bytes, size_t n, bool planned) {
-  Layout l;
-  const size_t max_passes = key_bytes;  // 8-bit digits
-  l.small = small_tiles(key_bytes, value_bytes, n, planned);
-  const size_t tile =
-      l.small ? small_tile_items(key_bytes, value_bytes) : tile_items(key_bytes, value_bytes);
-  l.tiles = (n + tile - 1) / tile;
-  l.desc_bytes = n < (size_t(1) << 30) ? 4 : 8;
-  size_t off = 0;
-  l.bins = off;
-  off += align_up(max_passes * BINS * sizeof(uint32_t), 256);
-  l.skew = off;
-  off += align_up(max_passes * sizeof(uint32_t), 256);
-  l.groups = (l.tiles + GROUP - 1) / GROUP;
-  l.lb_ginc = align_up(l.tiles * BINS * l.desc_bytes, 256);
-  l.lb_gagg = l.lb_ginc + align_up(l.groups * BINS * l.desc_bytes, 256);
-  l.lb_ticket = l.lb_gagg + align_up(l.groups * BINS * sizeof(uint32_t), 256);
-  l.lb_bytes = l.lb_ticket + align_up(XCDS * sizeof(uint32_t), 256);
-  l.lb[0] = off;
-  off += l.lb_bytes;
-  l.lb[1] = off;
-  off += l.lb_bytes;
-  l.total = n == 0 ? 0 : off;
-  return l;
-}
 
 namespace {
 
@@ -152,14 +127,24 @@ rccl_hip_status probe_device(DeviceCaps *caps) {
   for (int b = 0; b < XCC_PROBE_BLOCKS; ++b) round_robin &= host[1 + b] == uint32_t(b) % XCDS;
   caps->nx = round_robin ? XCDS : 1u;
   caps->rank = caps->lane_order ? Rank::LaneAtomic : Rank::MatchAny;
+  int dev = 0, cus = 0;
+  err = hipGetDevice(&dev);
+  if (err == hipSuccess)
+    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (err != hipSuccess || cus <= 0)
+    return set_hip_error(RCCL_HIP_ERROR_DRIVER, "radix device CU count", err);
+  caps->cus = static_cast<uint32_t>(cus);
   return ok();
 }
 
 } // namespace
 
 namespace {
-// The current device's probed caps, probing it on first use.
-rccl_hip_status probed_caps(DeviceCaps *caps) {
+// The current device's probed caps, probing it on first use. The probe
+// launches on the null stream and copies its result back synchronously, which
+// a stream under graph capture does not allow: a first use from a capturing
+// `stream` is refused (load the program on the device before capturing).
+rccl_hip_status probed_caps(DeviceCaps *caps, hipStream_t stream, bool check_capture) {
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "current device", err);
@@ -170,6 +155,14 @@ rccl_hip_status probed_caps(DeviceCaps *caps) {
       return ok();
     }
   }
+  if (check_capture) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    err = hipStreamIsCapturing(stream, &status);
+    if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "stream capture status", err);
+    if (status != hipStreamCaptureStatusNone)
+      return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT,
+                       "device not loaded before stream capture (rccl_hip_program_load)");
+  }
   RCCL_HIP_TRY(probe_device(caps));
   g_caps.push_back(CapsEntry{dev, *caps});
   return ok();
@@ -178,12 +171,12 @@ rccl_hip_status probed_caps(DeviceCaps *caps) {
 
 rccl_hip_status probe_current_device() {
   DeviceCaps caps;
-  return probed_caps(&caps);
+  return probed_caps(&caps, nullptr, false);
 }
 
-rccl_hip_status device_caps(DeviceCaps *caps) {
+rccl_hip_status device_caps(DeviceCaps *caps, hipStream_t stream) {
   DeviceCaps c;
-  RCCL_HIP_TRY(probed_caps(&c));
+  RCCL_HIP_TRY(probed_caps(&c, stream, true));
   switch (g_ranking.load(std::memory_order_relaxed)) {
   case RCCL_HIP_RANKING_LANE_ATOMIC:
     if (!c.lane_order)
@@ -200,9 +193,9 @@ rccl_hip_status device_caps(DeviceCaps *caps) {
 
 } // namespace radix
 
-rccl_hip_status tile_order(uint32_t *nx) {
+rccl_hip_status tile_order(uint32_t *nx, hipStream_t stream) {
   radix::DeviceCaps c;
-  RCCL_HIP_TRY(radix::device_caps(&c));
+  RCCL_HIP_TRY(radix::device_caps(&c, stream));
   *nx = c.nx;
   return ok();
 }

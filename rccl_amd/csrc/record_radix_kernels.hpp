@@ -330,15 +330,8 @@ rccl_hip_status run_radix(const RecordArgs &a) {
   b.vscratch = reinterpret_cast<Val *>(ws + l.scratch_vals);
 
   radix::DeviceCaps caps;
-  RCCL_HIP_TRY(radix::device_caps(&caps));
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    hipError_t err = hipGetDevice(&dev);
-    if (err == hipSuccess)
-      err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "record sort device", err);
-  }
+  RCCL_HIP_TRY(radix::device_caps(&caps, a.stream));
+  const size_t cus = caps.cus;
 
   {
     KernelTimer t("record_init", a.stream, 0);

@@ -47,12 +47,11 @@ rccl_hip_status rccl_hip_record_sort(uint32_t arity, size_t payload_bytes, const
   if (payload_bytes && (!in_payloads || !out_payloads))
     return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "record-sort payload");
   {
-    // Each stream in place (input == output) or into a disjoint output.
+    // Each stream in place (input == output) or into an output disjoint from
+    // both inputs and the other output.
     const size_t rb = sat_mul(n, 4u * size_t(arity)), pb = sat_mul(n, payload_bytes);
-    if ((in_rows != out_rows && ranges_overlap(in_rows, rb, out_rows, rb)) ||
-        (payload_bytes && in_payloads != out_payloads &&
-         ranges_overlap(in_payloads, pb, out_payloads, pb)) ||
-        ranges_overlap(out_rows, rb, out_payloads, pb))
+    if (sort_streams_overlap(in_rows, out_rows, rb, payload_bytes ? in_payloads : nullptr,
+                             payload_bytes ? out_payloads : nullptr, pb))
       return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "record-sort buffers overlap");
   }
   const record_sort::RecordArgs s{in_rows, in_payloads, out_rows, out_payloads, n,

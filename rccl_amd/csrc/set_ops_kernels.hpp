@@ -606,12 +606,11 @@ rccl_hip_status run_op(const SetArgs &s) {
   // Descriptors, group words and the ticket are contiguous.
   const size_t state_words = lookback::state_words(l.lb_tiles);
   uint32_t nx = 1;
-  RCCL_HIP_TRY(tile_order(&nx));
-  if (nx == XCDS)
-    RCCL_HIP_TRY(check_xcd_rows(
-        s.arith ? reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, SUB, true>)
-                : reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, SUB, false>),
-        THREADS, XCD_RUN, "set tile does not fit on the device"));
+  RCCL_HIP_TRY(tile_order(&nx, s.stream));
+  RCCL_HIP_TRY(fit_tile_order(
+      s.arith ? reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, SUB, true>)
+              : reinterpret_cast<const void *>(&tile_kernel<K, V, Cmp, OP, ITEMS, SUB, false>),
+      THREADS, XCD_RUN, &nx));
   const dim3 pgrid(static_cast<uint32_t>((l.tiles + 1 + 255) / 256));
   const dim3 tgrid(
       static_cast<uint32_t>(nx == XCDS ? xcd_order_grid(l.lb_tiles, XCD_RUN) : l.lb_tiles));

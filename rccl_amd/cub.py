@@ -49,21 +49,32 @@ class ComparatorNotLowered(ValueError):
 def _probe_keys(dtype):
     """Fixed probe keys for classifying a comparator over `dtype`: the type's
     extremes and their neighbours, zero and small values (runs of equal
-    decades and both parities), byte boundaries; for floats also the
-    infinities, signed zeros, denormals and the smallest normals."""
+    decades and both parities), byte boundaries, and for every bit k the
+    values 2^k - 1, 2^k and 2^k + 1 (and their negatives for signed types),
+    so that a closure that flips or masks one bit disagrees with the natural
+    order on some pair; for floats also the infinities, signed zeros,
+    denormals, the smallest normals, and every single-bit pattern with
+    either sign."""
     dt = np.dtype(dtype)
+    bits = 8 * dt.itemsize
     if dt.kind == "f":
         fi = np.finfo(dt)
         tiny, sub = float(fi.tiny), float(fi.smallest_subnormal)
         vals = [-np.inf, -float(fi.max), -1.5, -1.0, -tiny, -sub, -0.0, 0.0, sub, tiny, 0.5,
                 1.0, 1.5, 2.0, 10.0, 14.0, 15.0, 16.0, 25.0, 26.0, float(fi.max), np.inf]
+        ut = np.dtype(f"u{dt.itemsize}")
+        single = np.array([1 << k for k in range(bits - 1)], dtype=ut).view(dt)
+        single = single[np.isfinite(single)]
+        vals += [float(v) for v in single] + [-float(v) for v in single]
     else:
         ii = np.iinfo(dt)
         small = list(range(0, 22)) + [126, 127, 128, 129, 255, 256]
         vals = [ii.min, ii.min + 1, ii.max - 1, ii.max, ii.max // 2, ii.max // 2 + 1]
         vals += [v for v in small if v <= ii.max]
+        for k in range(bits):
+            vals += [v for v in ((1 << k) - 1, 1 << k, (1 << k) + 1) if v <= ii.max]
         if ii.min < 0:
-            vals += [-v for v in small if -v >= ii.min]
+            vals += [-v for v in vals if v > 0 and -v >= ii.min]
     # Distinct bit patterns (-0.0 and +0.0 both stay), as Python scalars
     # (float keys widen exactly), which is what a Python closure expects.
     arr = np.array(vals, dtype=dt)

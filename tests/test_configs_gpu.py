@@ -214,3 +214,42 @@ def test_c3_full_size_device_checks(launch):
     assert bool(torch.isposinf(rest[:counts["+inf"]]).all())
     assert bool(torch.isneginf(rest[rest.numel() - counts["-inf"]:]).all())
 
+
+
+# ---------------------------------------------------------------------------
+# The metric's own shapes (bench.py's headline and pairs legs).
+# ---------------------------------------------------------------------------
+def test_metric_u32_keys_full_size(launch):
+    """2^28 u32 keys ascending from bench.py's device generator: the output
+    equals the input sorted by torch.sort (unsigned order through a flipped
+    sign bit), word for word."""
+    import torch
+
+    n = 1 << 28
+    keys_t = wd.metric_u32_keys(n)
+    d = DeviceBuffer(keys_t.clone(), np.uint32, n)
+    ws = cub.device_radix_sort_workspace(launch, np.uint32, n)
+    cub.device_radix_sort_keys(launch, d, ws)
+    launch.synchronize()
+    sign = torch.tensor(-(1 << 31), dtype=torch.int32, device=keys_t.device)
+    want = torch.sort(keys_t ^ sign).values ^ sign
+    del keys_t
+    assert bool(torch.equal(d.tensor, want))
+
+
+def test_metric_pairs_full_size(launch):
+    """2^28 u64 keys with u32 values = original index, ascending, from
+    bench.py's device generator: keys non-decreasing, every value the index
+    of its own key, indices a permutation and rising within runs of equal
+    keys; together these fix the stable sort's output exactly."""
+    import torch
+
+    n = 1 << 28
+    keys_t, vals_t = wd.metric_pairs(n)
+    dk = DeviceBuffer(keys_t.clone(), np.uint64, n)
+    dv = DeviceBuffer(vals_t.clone(), np.uint32, n)
+    del vals_t
+    ws = cub.device_radix_sort_pairs_workspace(launch, np.uint64, np.uint32, n)
+    cub.device_radix_sort_pairs(launch, dk, dv, ws)
+    launch.synchronize()
+    _check_stable_pairs_device(torch, keys_t, dk.tensor, dv.tensor)

@@ -120,6 +120,20 @@ def test_overlapping_buffers_rejected(lib):
                                    FAKE, 1 << 30, None) == 9
     assert lib.rccl_hip_merge_sort(0, 0, 0, _ptr(base), None, _ptr(base), None, 100_000,
                                    FAKE, 1, None) == 2
+    # Merge sort pairs (copy form): an output over the other stream's input,
+    # or the two outputs over each other. u32 keys and values: 400,000 bytes
+    # per stream.
+    k_in, v_in, k_out, v_out = base, base + (1 << 20), base + (2 << 20), base + (3 << 20)
+    for ki, vi, ko, vo in [(k_in, v_in, k_out, k_in + 4000),   # values out over keys in
+                           (k_in, v_in, v_in + 400, v_out),    # keys out over values in
+                           (k_in, v_in, k_out, k_out + 4)]:    # outputs over each other
+        assert lib.rccl_hip_merge_sort(0, 4, 0, _ptr(ki), _ptr(vi), _ptr(ko), _ptr(vo), 100_000,
+                                       FAKE, 1 << 30, None) == 9
+        assert _last().role == b"merge sort buffers overlap"
+    # Disjoint copies, and both streams in place, pass that check.
+    for ki, vi, ko, vo in [(k_in, v_in, k_out, v_out), (k_in, v_in, k_in, v_in)]:
+        assert lib.rccl_hip_merge_sort(0, 4, 0, _ptr(ki), _ptr(vi), _ptr(ko), _ptr(vo), 100_000,
+                                       FAKE, 1, None) == 2
     # Set operations: an output over the second input, even with a huge capacity.
     for cap in (2 * n, (1 << 64) - 1):
         assert lib.rccl_hip_set_op(0, 0, 0, 0, _ptr(base), None, n, _ptr(base + 8192), None, n,
@@ -154,6 +168,15 @@ def test_overlapping_buffers_rejected_other_calls(lib):
     assert _last().role == b"record-sort buffers overlap"
     assert lib.rccl_hip_record_sort(4, 8, _ptr(base), _ptr(base + (1 << 28)), _ptr(base),
                                     _ptr(base + (1 << 28)), 100_000, FAKE, 1, None) == 2
+    # Record sort with payloads: payloads out over rows in, rows out over
+    # payloads in (rows of 16 bytes: 1,600,000 bytes; payloads 800,000).
+    r_in, p_in, r_out, p_out = base, base + (4 << 20), base + (8 << 20), base + (12 << 20)
+    for ri, pi, ro, po in [(r_in, p_in, r_out, r_in + 1000), (r_in, p_in, p_in + 8, p_out)]:
+        assert lib.rccl_hip_record_sort(4, 8, _ptr(ri), _ptr(pi), _ptr(ro), _ptr(po), 100_000,
+                                        FAKE, 1 << 30, None) == 9
+        assert _last().role == b"record-sort buffers overlap"
+    assert lib.rccl_hip_record_sort(4, 8, _ptr(r_in), _ptr(p_in), _ptr(r_out), _ptr(p_out),
+                                    100_000, FAKE, 1, None) == 2
 
 
 def test_merge_and_sort_validation(lib):
@@ -530,6 +553,46 @@ def test_comparator_classification():
         cub.order_code(total_cmp, np.float32)
     with pytest.raises(ValueError):
         cub.order_code(7)
+
+
+@pytest.mark.parametrize("dt", [np.uint8, np.int16, np.uint32, np.int32, np.uint64, np.int64])
+def test_comparator_single_bit_closures_rejected(dt):
+    """A closure that agrees with the natural order except through one bit (it
+    flips, masks or ignores bit k) is rejected for every bit of the key type:
+    the probe keys hold 2^k - 1, 2^k and 2^k + 1 for every k."""
+    from rccl_amd import cub
+
+    bits = 8 * np.dtype(dt).itemsize
+    signed = np.dtype(dt).kind == "i"
+    # (On Python's unbounded integers, flipping or clearing the sign bit of a
+    # signed key moves every negative key by the same amount: still the
+    # natural order, so that bit is not probed for signed types.)
+    for k in range(bits - 1 if signed else bits):
+        m = 1 << k
+        flip = lambda a, b, m=m: cub.ascending(a ^ m, b ^ m)
+        ignore = lambda a, b, m=m: cub.ascending(a & ~m, b & ~m)
+        for f in (flip, ignore):
+            with pytest.raises(cub.ComparatorNotLowered):
+                cub.order_code(f, dt)
+
+
+def test_comparator_single_bit_float_closures_rejected():
+    """The same for float keys compared through their bit patterns with one
+    bit of the pattern flipped."""
+    import struct
+
+    from rccl_amd import cub
+
+    for fmt, ifmt, bits, dt in (("<f", "<I", 32, np.float32), ("<d", "<Q", 64, np.float64)):
+        def key(x, m, fmt=fmt, ifmt=ifmt):
+            u = struct.unpack(ifmt, struct.pack(fmt, x))[0] ^ m
+            return struct.unpack(fmt, struct.pack(ifmt, u))[0]
+
+        for k in range(bits - 1):
+            m = 1 << k
+            f = lambda a, b, m=m: cub.ascending(key(a, m), key(b, m))
+            with pytest.raises(cub.ComparatorNotLowered):
+                cub.order_code(f, dt)
 
 
 def test_static_radix_rejects_oversized_before_any_launch(lib):

@@ -417,3 +417,26 @@ def test_merge_sort_radix_lowering_mixed_aliasing(launch, radix_ranking, kind, a
     launch.synchronize()
     np.testing.assert_array_equal(k_out.to_host_vec(), wk)
     np.testing.assert_array_equal(v_out.to_host_vec(), wv)
+
+
+@pytest.mark.parametrize("kind", ["u32", "f32"])
+@pytest.mark.parametrize("descending", [False, True])
+def test_merge_keys_tile_switch_at_2pow24(launch, kind, descending):
+    """Keys-only merges of 4-byte keys use 12-item tiles up to 2^24 outputs
+    and 16-item tiles above: both sides of the switch, and a larger merge
+    with heavy duplicates, against the oracle; the workspace (one split per
+    tile) shrinks across the switch."""
+    half = 1 << 23
+    shapes = [("at", half, half, None), ("past", half, half + 1, None),
+              ("dups", (1 << 23) + 12_345, (1 << 23) + (1 << 20), 5_000)]
+    for name, na, nb, distinct in shapes:
+        a = _sorted(kind, _random_keys(kind, na, 71, distinct), descending)
+        b = _sorted(kind, _random_keys(kind, nb, 72, distinct), descending)
+        got = _merge(launch, kind, a, b, descending=descending)
+        want = oracle.merge(kind, a, b, descending=descending)
+        assert np.array_equal(_bits(got), _bits(want)), (kind, name, descending)
+    from rccl_amd import _abi
+
+    at, past = (_abi.workspace_bytes("rccl_hip_merge_workspace_bytes", _abi.KEY_KINDS[kind], 0,
+                                     half, nb) for nb in (half, half + 1))
+    assert past < at, (at, past)

@@ -64,3 +64,41 @@ def test_static_float_descending_then_smaller(launch):
         got, _ = _sort(launch, "f32", keys, None, True, static=True)
         want = oracle.radix_sort("f32", keys, descending=True)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_static_sort_replayed_from_a_captured_graph(launch):
+    """The entry point's purpose: a sort inside a captured HIP graph. After the
+    program is loaded (and one eager call), the input restore and the static
+    sort are captured on a side stream, then the graph is replayed four
+    times with eager work (a static sort of other data, synchronizations)
+    between the replays; every replay must give the oracle's output."""
+    import torch
+
+    n = 1_000_003
+    keys = workloads.uniform_u32(n, 0xCA97)
+    keys[::5] = keys[1]  # ties
+    want = oracle.radix_sort("u32", keys)
+    pristine = DeviceBuffer.from_host(keys)
+    dk, sk = DeviceBuffer.zeroed(np.uint32, n), DeviceBuffer.zeroed(np.uint32, n)
+    lib = _abi.load()
+    kind = _abi.KEY_KINDS["u32"]
+    # Eager first: the device probe and the static workspace lookup happen
+    # outside the capture.
+    other = workloads.uniform_u32(70_001, 0xE6E)
+    got, _ = _sort(launch, "u32", other, None, False, static=True)
+    assert np.array_equal(got, oracle.radix_sort("u32", other))
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=side):
+        dk.tensor.copy_(pristine.tensor)
+        _abi.check(lib.rccl_hip_radix_sort_static(kind, 0, _abi.ASCENDING, dk.ptr, None, sk.ptr,
+                                                  None, n, torch.cuda.current_stream().cuda_stream))
+    for replay in range(4):
+        dk.tensor.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(dk.to_host_vec(), want), f"replay {replay}"
+        got, _ = _sort(launch, "u32", other, None, replay % 2 == 1, static=True)
+        assert np.array_equal(got, oracle.radix_sort("u32", other, descending=replay % 2 == 1))
