@@ -325,6 +325,11 @@ enum class Rank : int { LaneAtomic = 0, MatchAny = 1 };
 #ifndef RCCL_RADIX_SKEW_RANKING
 #define RCCL_RADIX_SKEW_RANKING 1
 #endif
+// Lanes of one item sharing lane 0's digit that make a wave take the skewed
+// ranking in a pass that is not skewed as a whole.
+#ifndef RCCL_RADIX_SKEW_LANES
+#define RCCL_RADIX_SKEW_LANES 8
+#endif
 // Items per batch of counter reads in the skewed ranking.
 #ifndef RCCL_RADIX_RANK_BATCH
 #define RCCL_RADIX_RANK_BATCH 8
@@ -523,6 +528,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   __shared__ uint32_t digit_off[BINS];
   __shared__ uint32_t wave_sum[BINS / 64];
   __shared__ uint32_t s_tile;
+  __shared__ uint32_t s_skew_waves;  // set when some wave takes the skewed ranking
   Bits *stage_keys = reinterpret_cast<Bits *>(stage_raw);
 
   const uint32_t tid = threadIdx.x;
@@ -539,6 +545,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   }
   if (tile >= num_tiles) return;
   for (uint32_t i = tid; i < WAVES * NB; i += THREADS) (&cnt[0][0])[i] = 0;
+  if (tid == 0) s_skew_waves = 0;
   // Global start of each digit's bucket (exclusive offsets from bins_scan).
   const uint32_t bin_start = tid < BINS ? pass_bins[tid] : 0u;
 
@@ -580,8 +587,9 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   // lane adding 64.
   //
   // Skewed passes (bins_scan_kernel flags a pass whose most frequent digit
-  // holds at least 1 / RCCL_RADIX_HOT_DIV of the keys; lane-ordered ranking
-  // only) count with returning atomics, whose results are the keys' ranks
+  // holds at least 1 / RCCL_RADIX_HOT_DIV of the keys), and skewed waves of
+  // other passes (below; lane-ordered ranking only), count with returning
+  // atomics, whose results are the keys' ranks
   // within their wave and digit. Each thread parks its ranks in its own slots
   // of the staging area (free until the keys are staged) and reads them back
   // after the count, so the ranking below reads each wave's digit start
@@ -589,21 +597,43 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   // where an atomic on a hot digit's counter is served lane by lane.
   uint32_t *wcnt = cnt[wave];
   constexpr bool SKEW_PATH = RANK == Rank::LaneAtomic && skew_ranking<Bits, Val, ITEMS>();
-  const bool skewed = SKEW_PATH && pass_skew && *pass_skew != 0;
+  bool skewed = SKEW_PATH && pass_skew && *pass_skew != 0;
+  if (SKEW_PATH && !skewed) {
+    // A wave of a pass that is not skewed as a whole can still hold a skewed
+    // stretch of the input (the previous pass gathers equal digits into
+    // neighbouring tiles). The wave takes the skewed path when, in its first
+    // or middle item, at least RCCL_RADIX_SKEW_LANES lanes (but not all 64)
+    // share lane 0's digit.
+    auto shared_with_lane0 = [&](int j) {
+      const uint32_t d =
+          uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
+      return static_cast<uint32_t>(
+          __builtin_popcountll(__ballot(d == __builtin_amdgcn_readfirstlane(d))));
+    };
+    const uint32_t m0 = shared_with_lane0(0), m1 = shared_with_lane0(ITEMS / 2);
+    skewed = (m0 >= RCCL_RADIX_SKEW_LANES && m0 < 64) || (m1 >= RCCL_RADIX_SKEW_LANES && m1 < 64);
+  }
+  if (skewed && lane == 0) s_skew_waves = 1;
   uint32_t *rank_slot = reinterpret_cast<uint32_t *>(stage_raw) + wave * WAVE_ITEMS + lane;
   uint32_t pos[ITEMS];
   if (skewed) {
+    // The lanes sharing lane 0's digit (a whole wave-uniform item, or a hot
+    // digit's group) take one atomic: lane 0 adds the group's size, and each
+    // of the others is lane 0's base plus its group lanes below (marked with
+    // PEER until the bases return). Every other lane takes its own atomic.
+    constexpr uint32_t PEER = 1u << 31;
     uint32_t ret[ITEMS];
-    uint64_t uniform = 0;
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
       const uint32_t d =
           uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
-      if (wave_uniform(d)) {
-        uniform |= uint64_t(1) << j;
-        ret[j] = lane == 0 ? __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_WORKGROUP)
-                           : 0u;
+      const bool in_group = d == __builtin_amdgcn_readfirstlane(d);
+      const uint64_t group = __ballot(in_group);
+      if (in_group) {
+        ret[j] = lane == 0 ? __hip_atomic_fetch_add(
+                                 &wcnt[d], static_cast<uint32_t>(__builtin_popcountll(group)),
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                           : PEER | popc_below(group);
       } else {
         ret[j] =
             __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -611,8 +641,8 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     }
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
-      if (uniform & (uint64_t(1) << j)) ret[j] = __builtin_amdgcn_readfirstlane(ret[j]) + lane;
-      rank_slot[j * 64] = ret[j];
+      const uint32_t base = __builtin_amdgcn_readfirstlane(ret[j]);
+      rank_slot[j * 64] = (ret[j] & PEER) ? base + (ret[j] & ~PEER) : ret[j];
     }
   } else {
 #pragma unroll
@@ -628,6 +658,8 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     }
   }
   lds_barrier();
+  // Whether some wave of the block parked its ranks in the staging area.
+  const bool block_skew = SKEW_PATH && s_skew_waves != 0;
 
   // Per digit: the tile's count, published at once together with the first
   // look-back windows (consumed after the ranking, so their latency hides
@@ -716,62 +748,67 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
         stage_keys[pos[j]] = key[j];
       }
     }
-  } else if (skewed) {
-    // Position = the wave's start for the digit + the rank from the count.
-    // Every thread reads its parked ranks before any key is staged over them.
+  } else {
+    // Where some wave of the block parked its ranks, every parked rank is read
+    // before any key is staged over it: each wave passes one barrier (the
+    // skewed flag is the same in all lanes of a wave).
+    if (skewed) {
+      // Position = the wave's start for the digit + the rank from the count.
 #pragma unroll
-    for (int j = 0; j < ITEMS; ++j) pos[j] = rank_slot[j * 64];
-    lds_barrier();
-    // In batches: a batch's counter reads are issued together, then its keys
-    // staged (all at once would hold a second register per key).
-    constexpr int RB = RCCL_RADIX_RANK_BATCH;
+      for (int j = 0; j < ITEMS; ++j) pos[j] = rank_slot[j * 64];
+      lds_barrier();
+      // In batches: a batch's counter reads are issued together, then its keys
+      // staged (all at once would hold a second register per key).
+      constexpr int RB = RCCL_RADIX_RANK_BATCH;
 #pragma unroll
-    for (int j0 = 0; j0 < ITEMS; j0 += RB) {
-      uint32_t start[RB];
+      for (int j0 = 0; j0 < ITEMS; j0 += RB) {
+        uint32_t start[RB];
 #pragma unroll
-      for (int j = j0; j < j0 + RB && j < ITEMS; ++j) {
+        for (int j = j0; j < j0 + RB && j < ITEMS; ++j) {
+          const uint32_t d =
+              uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
+          start[j - j0] = wcnt[d];
+        }
+#pragma unroll
+        for (int j = j0; j < j0 + RB && j < ITEMS; ++j) asm volatile("" : "+v"(start[j - j0]));
+#pragma unroll
+        for (int j = j0; j < j0 + RB && j < ITEMS; ++j) {
+          pos[j] = min(pos[j] + start[j - j0], uint32_t(TILE));
+          stage_keys[pos[j]] = key[j];
+        }
+      }
+    } else {
+      if (block_skew) lds_barrier();
+      // The returning atomic hands equal digits consecutive positions in lane
+      // order. All atomics are issued before the first staging write, so the
+      // round trips overlap; the opaque copy of the positions keeps the
+      // compiler from pairing each write with its atomic (which serialises
+      // them). A wave-uniform digit takes 64 consecutive positions with one
+      // atomic: lane l's is the returned base + l, as the lane-ordered atomic
+      // would give.
+      uint64_t uniform = 0;
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j) {
         const uint32_t d =
             uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
-        start[j - j0] = wcnt[d];
+        if (wave_uniform(d)) {
+          uniform |= uint64_t(1) << j;
+          pos[j] = lane == 0 ? __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_WORKGROUP)
+                             : 0u;
+        } else {
+          pos[j] =
+              __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
       }
 #pragma unroll
-      for (int j = j0; j < j0 + RB && j < ITEMS; ++j) asm volatile("" : "+v"(start[j - j0]));
+      for (int j = 0; j < ITEMS; ++j) asm volatile("" : "+v"(pos[j]));
 #pragma unroll
-      for (int j = j0; j < j0 + RB && j < ITEMS; ++j) {
-        pos[j] = min(pos[j] + start[j - j0], uint32_t(TILE));
+      for (int j = 0; j < ITEMS; ++j) {
+        if (uniform & (uint64_t(1) << j)) pos[j] = __builtin_amdgcn_readfirstlane(pos[j]) + lane;
+        pos[j] = min(pos[j], uint32_t(TILE));
         stage_keys[pos[j]] = key[j];
       }
-    }
-  } else {
-    // The returning atomic hands equal digits consecutive positions in lane
-    // order. All atomics are issued before the first staging write, so the
-    // round trips overlap; the opaque copy of the positions keeps the
-    // compiler from pairing each write with its atomic (which serialises
-    // them). A wave-uniform digit takes 64 consecutive positions with one
-    // atomic: lane l's is the returned base + l, as the lane-ordered atomic
-    // would give.
-    uint64_t uniform = 0;
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      const uint32_t d =
-          uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
-      if (wave_uniform(d)) {
-        uniform |= uint64_t(1) << j;
-        pos[j] = lane == 0 ? __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_WORKGROUP)
-                           : 0u;
-      } else {
-        pos[j] =
-            __hip_atomic_fetch_add(&wcnt[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) asm volatile("" : "+v"(pos[j]));
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      if (uniform & (uint64_t(1) << j)) pos[j] = __builtin_amdgcn_readfirstlane(pos[j]) + lane;
-      pos[j] = min(pos[j], uint32_t(TILE));
-      stage_keys[pos[j]] = key[j];
     }
   }
 

@@ -498,3 +498,30 @@ def test_skewed_digits_pairs_stable(launch, nhot, descending):
     want_k, want_v = oracle.radix_sort("u64", keys, vals, descending=descending)
     np.testing.assert_array_equal(got_k, want_k)
     np.testing.assert_array_equal(got_v, want_v)
+
+
+@pytest.mark.parametrize("kind", ["u32", "f32", "u64"])
+@pytest.mark.parametrize("descending", [False, True])
+def test_locally_skewed_stretch(launch, kind, descending):
+    """A pass that is not skewed as a whole (no digit holds 1/16 of the keys)
+    but has a skewed stretch: 5% of the input, contiguous, is 80% one value.
+    Waves in that stretch take the skewed ranking on their own, others the
+    uniform one, in the same blocks."""
+    dt = np.dtype(oracle.KIND_DTYPES[kind])
+    n = 1_000_003
+    bits = workloads.hash_range(0x10CA1, n)
+    lo, hi = 300_001, 300_001 + n // 20
+    pick = workloads.hash_range(0x10CA2, hi - lo) % np.uint64(5)
+    bits[lo:hi] = np.where(pick < np.uint64(4), bits[lo], bits[lo:hi])
+    if dt.itemsize == 4:
+        bits = (bits >> np.uint64(32)).astype(np.uint32)
+    host = bits.view(dt)
+    got = _sort_keys(launch, host, descending)
+    want = oracle.radix_sort(kind, host, descending=descending)
+    np.testing.assert_array_equal(_bits(got), _bits(want))
+    if kind == "u64":
+        vals = np.arange(n, dtype=np.uint32)
+        gk, gv = _sort_pairs(launch, host, vals, descending)
+        wk, wv = oracle.radix_sort("u64", host, vals, descending=descending)
+        np.testing.assert_array_equal(gk, wk)
+        np.testing.assert_array_equal(gv, wv)
