@@ -112,12 +112,14 @@ template <> struct DescInfo<uint64_t> {
 };
 
 // Two-level look-back state of one pass. Tiles form groups of GROUP; besides
-// its own descriptor, every tile adds (1 << GAGG_SHIFT) | count to its
-// group's per-digit aggregate word, which is therefore complete exactly when
-// its top byte equals the group size. The group's last tile also publishes
-// the inclusive prefix through the group. A look-back sums in-group
-// predecessors tile by tile and earlier groups whole, so the prefix chain
-// advances a group per step instead of a tile.
+// its own descriptor (its count; tile 0's is inclusive), every tile adds
+// (1 << GAGG_SHIFT) | count to its group's per-digit aggregate word, which is
+// therefore complete exactly when its top byte equals the group size. Only
+// the group's last tile publishes an inclusive prefix, through the group
+// (an inclusive descriptor per tile measured no faster: look-backs rarely
+// found one, and its stores added 1 KB of writes per tile). A look-back sums
+// in-group predecessors tile by tile and earlier groups whole, so the prefix
+// chain advances a group per step instead of a tile.
 constexpr int GAGG_SHIFT = 24;
 constexpr uint32_t GAGG_MASK = (1u << GAGG_SHIFT) - 1;
 template <class Desc> struct LookbackBuf {
@@ -821,7 +823,6 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     const Desc excl = lookback_consume<Desc>(lbuf, tile, group, tid, lb, gi, ga);
     wait_vmcnt<0>();
     const Desc incl = static_cast<Desc>(DI::INCL | (excl + Desc(count)));
-    if (tile > 0) store_agent(&lbuf.tile[size_t(tile) * BINS + tid], incl);
     const uint32_t glast = min(uint32_t(gfirst + GROUP), num_tiles) - 1u;
     if (tile == glast) store_agent(&lbuf.ginc[size_t(group) * BINS + tid], incl);
     digit_off[tid] = bin_start + static_cast<uint32_t>(excl) - tile_start;
