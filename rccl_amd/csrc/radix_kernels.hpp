@@ -167,22 +167,37 @@ constexpr int hist_cols() {
   return HIST_COLS_4B * 4 / int(sizeof(Bits));
 }
 
+// 8-byte keys are loaded 16 bytes (two keys) per lane and instruction (the
+// histogram counts keys in any order): C2's u64 histogram 130 -> 120 us at
+// 2^26. 4-byte keys keep one key per lane: four per load measured 3-5 us
+// slower at 2^28 u32. (16-bit counters packed two per word, twice the
+// columns in the same LDS, measured slower for every key width: 2^28 u32
+// 212 -> 272 us.)
+#ifndef RCCL_RADIX_HIST_VLOAD_8B
+#define RCCL_RADIX_HIST_VLOAD_8B 1
+#endif
+typedef unsigned int hist_v4u __attribute__((ext_vector_type(4)));
+
 template <class Bits, class Ops>
 __global__ void __launch_bounds__(HIST_THREADS)
 histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__ bins,
                  uint32_t begin_bit, uint32_t end_bit, uint32_t passes,
                  uint32_t *__restrict__ zero_words, size_t zero_count) {
   constexpr int PMAX = int(sizeof(Bits));  // 8-bit passes
-  constexpr int HIST_COLS = hist_cols<Bits>();
-  __shared__ uint32_t hist[PMAX * BINS * HIST_COLS];  // [pass][digit][column]
+  constexpr bool VLOAD = sizeof(Bits) == 8 && RCCL_RADIX_HIST_VLOAD_8B;
+  constexpr int COLS = hist_cols<Bits>();
+  constexpr int WORDS = PMAX * BINS * COLS;
+  constexpr int VEC = VLOAD ? 16 / int(sizeof(Bits)) : 1;  // keys per load
+  constexpr int LOADS = HIST_ITEMS / VEC;
+  __shared__ uint32_t hist[WORDS];  // [pass][digit][column]
   const uint32_t tid = threadIdx.x;
-  for (uint32_t i = tid; i < passes * BINS * HIST_COLS; i += HIST_THREADS) hist[i] = 0;
+  for (uint32_t i = tid; i < WORDS; i += HIST_THREADS) hist[i] = 0;
   for (size_t i = size_t(blockIdx.x) * HIST_THREADS + tid; i < zero_count;
        i += size_t(gridDim.x) * HIST_THREADS)
     zero_words[i] = 0;
   __syncthreads();
 
-  const uint32_t col = tid % HIST_COLS;
+  const uint32_t col = tid % COLS;
   uint32_t shift[PMAX], dmask[PMAX];
 #pragma unroll
   for (int p = 0; p < PMAX; ++p) {
@@ -190,46 +205,66 @@ histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__
     shift[p] = bit;
     dmask[p] = uint32_t(p) < passes ? (1u << min(8u, end_bit - bit)) - 1u : 0u;
   }
+  auto count = [&](Bits key) {
+    const Bits s = Ops::digit_source(key);
+#pragma unroll
+    for (int p = 0; p < PMAX; ++p) {
+      if (uint32_t(p) >= passes) break;
+      const uint32_t d = static_cast<uint32_t>(s >> shift[p]) & dmask[p];
+      __hip_atomic_fetch_add(&hist[(uint32_t(p) * BINS + d) * COLS + col], 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
+  // With vector loads, the keys before the first 16-byte boundary and after
+  // the last whole vector are counted by block 0, one per thread.
+  const size_t head = VLOAD ? min<size_t>(
+      ((16u - (reinterpret_cast<uintptr_t>(keys) & 15u)) & 15u) / sizeof(Bits), n) : 0;
+  const size_t nvec = (n - head) / VEC;
+  const size_t tail = head + nvec * VEC;
+  if (VLOAD && blockIdx.x == 0) {
+    if (tid < head) count(keys[tid]);
+    else if (tid - head < n - tail) count(keys[tail + (tid - head)]);
+  }
+  using LoadT = typename std::conditional<VLOAD, hist_v4u, Bits>::type;
+  const LoadT *src = reinterpret_cast<const LoadT *>(keys + head);
   // The next chunk's keys are loaded before the current chunk is counted, so
   // the load latency hides behind the counting.
-  constexpr size_t CHUNK = size_t(HIST_THREADS) * HIST_ITEMS;
+  constexpr size_t CHUNK = size_t(HIST_THREADS) * LOADS;  // loads per chunk
   const size_t stride = size_t(gridDim.x) * CHUNK;
-  Bits next[HIST_ITEMS];
+  LoadT next[LOADS];
   auto load_chunk = [&](size_t base) {
-    const uint32_t avail = static_cast<uint32_t>(min<size_t>(n - base, CHUNK));
+    const uint32_t avail = static_cast<uint32_t>(min<size_t>(nvec - base, CHUNK));
 #pragma unroll
-    for (int j = 0; j < HIST_ITEMS; ++j)
-      next[j] = stream_load<RCCL_RADIX_HIST_NT>(
-          &keys[base + min(uint32_t(j) * HIST_THREADS + tid, avail - 1u)]);
+    for (int j = 0; j < LOADS; ++j) {
+      const LoadT *ptr = &src[base + min(uint32_t(j) * HIST_THREADS + tid, avail - 1u)];
+      if constexpr (VLOAD) next[j] = __builtin_nontemporal_load(ptr);
+      else next[j] = stream_load<RCCL_RADIX_HIST_NT>(ptr);
+    }
   };
-  if (size_t(blockIdx.x) * CHUNK < n) load_chunk(size_t(blockIdx.x) * CHUNK);
-  for (size_t base = size_t(blockIdx.x) * CHUNK; base < n; base += stride) {
-    const uint32_t avail = static_cast<uint32_t>(min<size_t>(n - base, CHUNK));
-    Bits k[HIST_ITEMS];
+  if (size_t(blockIdx.x) * CHUNK < nvec) load_chunk(size_t(blockIdx.x) * CHUNK);
+  for (size_t base = size_t(blockIdx.x) * CHUNK; base < nvec; base += stride) {
+    const uint32_t avail = static_cast<uint32_t>(min<size_t>(nvec - base, CHUNK));
+    LoadT k[LOADS];
 #pragma unroll
-    for (int j = 0; j < HIST_ITEMS; ++j) k[j] = next[j];
-    if (base + stride < n) load_chunk(base + stride);
+    for (int j = 0; j < LOADS; ++j) k[j] = next[j];
+    if (base + stride < nvec) load_chunk(base + stride);
 #pragma unroll
-    for (int j = 0; j < HIST_ITEMS; ++j) {
+    for (int j = 0; j < LOADS; ++j) {
       if (uint32_t(j) * HIST_THREADS + tid >= avail) continue;
-      const Bits s = Ops::digit_source(k[j]);
+      Bits kv[VEC];
+      __builtin_memcpy(kv, &k[j], sizeof(LoadT));
 #pragma unroll
-      for (int p = 0; p < PMAX; ++p) {
-        if (uint32_t(p) >= passes) break;
-        const uint32_t d = static_cast<uint32_t>(s >> shift[p]) & dmask[p];
-        __hip_atomic_fetch_add(&hist[(uint32_t(p) * BINS + d) * HIST_COLS + col], 1u,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
+      for (int e = 0; e < VEC; ++e) count(kv[e]);
     }
   }
   __syncthreads();
   // Row sums. Thread e reads its row's columns in rotated order, so the
   // threads of a wave read distinct banks.
   for (uint32_t e = tid; e < passes * BINS; e += HIST_THREADS) {
-    const uint32_t *row = &hist[e * HIST_COLS];
+    const uint32_t *row = &hist[e * COLS];
     uint32_t sum = 0;
 #pragma unroll
-    for (uint32_t c = 0; c < HIST_COLS; ++c) sum += row[(c + e) % HIST_COLS];
+    for (uint32_t c = 0; c < uint32_t(COLS); ++c) sum += row[(c + e) % COLS];
     if (sum) add_agent(&bins[e], sum);
   }
 }

@@ -525,3 +525,30 @@ def test_locally_skewed_stretch(launch, kind, descending):
         wk, wv = oracle.radix_sort("u64", host, vals, descending=descending)
         np.testing.assert_array_equal(gk, wk)
         np.testing.assert_array_equal(gv, wv)
+
+
+@pytest.mark.parametrize("n", [1_000_003, 3 * 17_408 + 1, 65_537])
+def test_u64_keys_off_16_byte_boundary(launch, n):
+    """8-byte keys whose buffer starts 8 bytes past a 16-byte boundary (the
+    histogram loads two keys per lane from the first 16-byte boundary on and
+    counts the key before it separately), keys-only and pairs."""
+    import torch
+
+    host = workloads.hash_range(0x0FF5E7, n + 1)
+    big = torch.from_numpy(host.view(np.int64)).to("cuda")
+    view = big[1:]  # 8 bytes past the allocation's start
+    assert view.data_ptr() % 16 == 8
+    keys = DeviceBuffer(view, np.uint64, n)
+    ws = cub.device_radix_sort_workspace(launch, np.uint64, n)
+    cub.device_radix_sort_keys(launch, keys, ws)
+    launch.synchronize()
+    np.testing.assert_array_equal(keys.to_host_vec(), oracle.radix_sort("u64", host[1:]))
+    big.copy_(torch.from_numpy(host.view(np.int64)))
+    vals = DeviceBuffer.from_host(np.arange(n, dtype=np.uint32))
+    keys = DeviceBuffer(big[1:], np.uint64, n)
+    ws = cub.device_radix_sort_pairs_workspace(launch, np.uint64, np.uint32, n)
+    cub.device_radix_sort_pairs(launch, keys, vals, ws)
+    launch.synchronize()
+    wk, wv = oracle.radix_sort("u64", host[1:], np.arange(n, dtype=np.uint32))
+    np.testing.assert_array_equal(keys.to_host_vec(), wk)
+    np.testing.assert_array_equal(vals.to_host_vec(), wv)
