@@ -278,51 +278,64 @@ histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__
 
 // Turn every pass's digit counts into exclusive offsets (the first output
 // position of each digit), once, so the onesweep blocks read them instead of
-// each scanning the bins. One block of BINS threads. With a plan, it also
-// marks the trivial passes (a digit counting all n keys) and writes the pass
-// plan. A separate launch: folding it into the histogram's last block (a
+// each scanning the bins. One block of BINS threads; MAXP bounds the passes
+// (the key's bytes). Every pass's counts are loaded at once and scanned with
+// one barrier. It also writes each pass's skew word and, with a plan, marks
+// the trivial passes (a digit counting all n keys) and writes the pass plan.
+// A separate launch: folding it into the histogram's last block (a
 // device-scope completion counter) measured slower at 2^28 (229 against 216
 // us), as the agent-scope release writes back every block's dirty L2 lines.
 // (Internal linkage, like init_kernel.)
 namespace {
+template <int MAXP>
 __global__ void __launch_bounds__(BINS)
 bins_scan_kernel(uint32_t *bins, uint32_t passes, uint32_t n, PassPlan *plan,
                  uint32_t plan_flags, uint32_t *skew) {
-  __shared__ uint32_t s_wave[BINS / 64];
-  __shared__ uint32_t s_top[BINS / 64];
-  __shared__ uint32_t s_trivial;
+  constexpr int WAVES = BINS / 64;
+  __shared__ uint32_t s_wave[MAXP][WAVES];  // per wave: its digits' total
+  __shared__ uint32_t s_top[MAXP][WAVES];   // per wave: its largest digit count
+  __shared__ uint32_t s_full[WAVES];        // per wave: passes with a digit of n keys
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
-  if (tid == 0) s_trivial = 0;
-  __syncthreads();
-  // Largest digit count of the pass.
-  auto block_max = [&](uint32_t v) {
+  const uint32_t wave = tid >> 6;
+  uint32_t c[MAXP], inc[MAXP];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, o, 64)));
-    if (lane == 0) s_top[tid >> 6] = v;
-    __syncthreads();
-    uint32_t m = s_top[0];
+  for (int p = 0; p < MAXP; ++p) c[p] = uint32_t(p) < passes ? bins[p * BINS + tid] : 0u;
+  uint32_t full = 0;
 #pragma unroll
-    for (int w = 1; w < BINS / 64; ++w) m = max(m, s_top[w]);
-    __syncthreads();
-    return uint64_t(m);
-  };
-  for (uint32_t p = 0; p < passes; ++p) {
-    const uint32_t c = bins[p * BINS + tid];
-    if (plan && c == n) atomicOr(&s_trivial, 1u << p);
-    const uint32_t inc = wave_inclusive_sum(c, lane);
-    if (lane == 63) s_wave[tid >> 6] = inc;
-    __syncthreads();
-    uint32_t excl = inc - c;
-    for (uint32_t w = 0; w < (tid >> 6); ++w) excl += s_wave[w];
-    bins[p * BINS + tid] = excl;
-    __syncthreads();
-    if (skew) {
-      const uint64_t top = block_max(c);
-      if (tid == 0) skew[p] = top * RCCL_RADIX_HOT_DIV >= uint64_t(n) ? 1u : 0u;
-    }
+  for (int p = 0; p < MAXP; ++p) {
+    inc[p] = wave_inclusive_sum(c[p], lane);
+    uint32_t top = c[p];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+      top = max(top, static_cast<uint32_t>(__shfl_xor(static_cast<int>(top), o, 64)));
+    if (__ballot(c[p] == n) != 0) full |= 1u << p;
+    if (lane == 63) s_wave[p][wave] = inc[p];
+    if (lane == 0) s_top[p][wave] = top;
   }
-  if (plan && tid == 0) assign_plan(static_cast<int>(passes), s_trivial, plan_flags, plan);
+  if (lane == 0) s_full[wave] = full;
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < MAXP; ++p) {
+    if (uint32_t(p) >= passes) break;
+    uint32_t excl = inc[p] - c[p];
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w)
+      if (uint32_t(w) < wave) excl += s_wave[p][w];
+    bins[p * BINS + tid] = excl;
+  }
+  if (skew && tid < passes) {
+    uint32_t top = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) top = max(top, s_top[tid][w]);
+    skew[tid] = uint64_t(top) * RCCL_RADIX_HOT_DIV >= uint64_t(n) ? 1u : 0u;
+  }
+  if (plan && tid == 0) {
+    uint32_t trivial = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) trivial |= s_full[w];
+    assign_plan(static_cast<int>(passes), trivial, plan_flags, plan);
+  }
 }
 } // namespace
 
@@ -585,6 +598,10 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   if (tid == 0) s_skew_waves = 0;
   // Global start of each digit's bucket (exclusive offsets from bins_scan).
   const uint32_t bin_start = tid < BINS ? pass_bins[tid] : 0u;
+  // The pass's skew word, read before the keys so its latency hides behind
+  // theirs (the skewed ranking below).
+  constexpr bool SKEW_PATH = RANK == Rank::LaneAtomic && skew_ranking<Bits, Val, ITEMS>();
+  const bool pass_skewed = SKEW_PATH && pass_skew && *pass_skew != 0;
 
   // Wave-contiguous, lane-striped load: item j of lane l is key
   // wave_base + 64 j + l, so (wave, item, lane) order is source order. Loads
@@ -633,8 +650,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   // instead of adding to it: a read that many lanes share is served once,
   // where an atomic on a hot digit's counter is served lane by lane.
   uint32_t *wcnt = cnt[wave];
-  constexpr bool SKEW_PATH = RANK == Rank::LaneAtomic && skew_ranking<Bits, Val, ITEMS>();
-  bool skewed = SKEW_PATH && pass_skew && *pass_skew != 0;
+  bool skewed = pass_skewed;
   if (SKEW_PATH && !skewed) {
     // A wave of a pass that is not skewed as a whole can still hold a skewed
     // stretch of the input (the previous pass gathers equal digits into
@@ -1256,8 +1272,11 @@ rccl_hip_status run_passes(SortArgs &a, const Layout &l, uint32_t passes) {
   RCCL_HIP_TRY(check_launch("radix histogram"));
   {
     KernelTimer t("radix_bins_scan", a.stream, passes * BINS);
-    bins_scan_kernel<<<1, BINS, 0, a.stream>>>(bins, passes, static_cast<uint32_t>(a.n), plan,
-                                                a.plan_flags, skew);
+    static_assert(sizeof(Bits) <= 8, "one pass per key byte");
+    if (passes > sizeof(Bits))
+      return set_error(RCCL_HIP_ERROR_INVALID_ARGUMENT, "radix passes", sizeof(Bits), passes);
+    bins_scan_kernel<int(sizeof(Bits))><<<1, BINS, 0, a.stream>>>(
+        bins, passes, static_cast<uint32_t>(a.n), plan, a.plan_flags, skew);
   }
   RCCL_HIP_TRY(check_launch("radix bins scan"));
   constexpr int ITEMS = items_for(sizeof(Bits), VBYTES);
