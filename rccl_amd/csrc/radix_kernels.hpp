@@ -605,24 +605,35 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
 
   // Wave-contiguous, lane-striped load: item j of lane l is key
   // wave_base + 64 j + l, so (wave, item, lane) order is source order. Loads
-  // are clamped instead of predicated; items past the end rank as dummies
-  // whatever they hold.
-  const size_t last_item = n - 1;
-  const size_t wave_base = size_t(tile) * TILE + size_t(wave) * WAVE_ITEMS;
+  // are clamped to the wave's last valid item instead of predicated (a wave
+  // past the end reads the input's last key); items past the end rank as
+  // dummies whatever they hold. Addresses are a wave-uniform base plus a
+  // 32-bit item index.
+  const size_t wave_base =
+      size_t(tile) * TILE + size_t(__builtin_amdgcn_readfirstlane(wave)) * WAVE_ITEMS;
+  const uint32_t wave_valid =
+      n > wave_base ? static_cast<uint32_t>(n - wave_base < WAVE_ITEMS ? n - wave_base
+                                                                       : size_t(WAVE_ITEMS))
+                    : 0u;
+  const size_t load_base = wave_valid ? wave_base : n - 1;
+  const uint32_t last_in_wave = wave_valid ? wave_valid - 1 : 0u;
+  const Bits *kp = keys_in + load_base;
+  // An opaque copy of the lane: the load indices then share nothing with the
+  // validity tests below, so they are not kept alive until those run.
+  uint32_t load_lane = lane;
+  asm("" : "+v"(load_lane));
   Bits key[ITEMS];
 #pragma unroll
   for (int j = 0; j < ITEMS; ++j)
     key[j] = stream_load<!PAIRS || RCCL_RADIX_NT_PAIR_KEYS>(
-        &keys_in[min(wave_base + size_t(j) * 64 + lane, last_item)]);
+        &kp[min(uint32_t(j * 64) + load_lane, last_in_wave)]);
   ValReg val[ITEMS];
   if constexpr (PAIRS) {
     // Issued now, consumed after the key scatter.
+    const Val *vp = vals_in + load_base;
 #pragma unroll
-    for (int j = 0; j < ITEMS; ++j)
-      val[j] = vals_in[min(wave_base + size_t(j) * 64 + lane, last_item)];
+    for (int j = 0; j < ITEMS; ++j) val[j] = vp[min(uint32_t(j * 64) + load_lane, last_in_wave)];
   }
-  const uint32_t wave_valid =
-      n > wave_base ? static_cast<uint32_t>(min<size_t>(n - wave_base, WAVE_ITEMS)) : 0u;
   lds_barrier();
   // Wait for all the keys (not the values) before counting: one wait here is
   // measurably faster than the per-item waits the compiler would interleave
@@ -947,6 +958,9 @@ onesweep_kernel(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
                 const uint32_t *__restrict__ pass_skew, LookbackBuf<Desc> lbuf,
                 LookbackBuf<Desc> lbuf_next, uint32_t nx, uint32_t bit, uint32_t mask,
                 uint32_t conv) {
+  // Never null here (only the record sort passes none): no branch around its
+  // load before the keys'.
+  __builtin_assume(pass_skew != nullptr);
   onesweep_tile<Bits, Val, Ops, ITEMS, Desc, THREADS, RANK>(keys_in, keys_out, vals_in, vals_out,
                                                             n, num_tiles, pass_bins, pass_skew,
                                                             lbuf, lbuf_next, nx, bit, mask, conv);
@@ -970,6 +984,7 @@ planned_onesweep_kernel(PlanBuffers<Bits, Val> b, size_t n, uint32_t num_tiles,
                         const uint32_t *__restrict__ pass_skew, const PassPlan *__restrict__ plan,
                         LookbackBuf<Desc> lb0, LookbackBuf<Desc> lb1, uint32_t nx, uint32_t bit,
                         uint32_t mask) {
+  __builtin_assume(pass_skew != nullptr);
   const PassPlan pl = *plan;
   if (!pl.active) return;
   const Bits *kin = pl.src == 0 ? b.in : (pl.src == 1 ? b.out : b.scratch);
