@@ -135,9 +135,11 @@ RCCL_HIP_API int rccl_hip_abi_version(void);
  * Program::load (rccl-cub/src/cuda.rs:749-756, rccl-thrust/src/cuda.rs:85-91)
  * and the target gate ensure_radix_target (rccl-cub/src/radix.rs:14-22).
  * Returns UNSUPPORTED_TARGET on any other architecture. On first use of a
- * device it also runs a one-block check that the LDS serves the lanes of one
- * atomic hitting the same address in lane order (the radix ranking relies on
- * it) and returns UNSUPPORTED_TARGET if it does not. */
+ * device it also checks, on every CU at once, that the LDS serves the lanes
+ * of one atomic hitting the same address in lane order (the default radix
+ * ranking relies on it); where it does not, the radix sorts rank by wave
+ * match-any instead, with the same results (forcing the lane-ordered ranking
+ * with rccl_hip_radix_configure then fails with UNSUPPORTED_TARGET). */
 RCCL_HIP_API rccl_hip_status rccl_hip_program_load(int device);
 
 /* ------------------------------------------------------------------------

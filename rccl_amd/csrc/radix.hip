@@ -48,17 +48,23 @@ rccl_hip_status static_workspace(void **out) {
 
 namespace {
 
-// Outputs of the one-time device probes below (no allocation needed).
-constexpr int XCC_PROBE_BLOCKS = 256;
-__device__ uint32_t probe_out[1 + XCC_PROBE_BLOCKS];
-
 // Lane-order self-check (see the onesweep notes): each wave repeatedly adds 1
-// to per-wave LDS counters chosen by a hash of (round, lane) restricted to
-// 1, 2, 16 or 256 counters, and checks that lanes hitting the same counter
-// received consecutive values in lane order. One block of CHECK_THREADS;
-// the number of violations is written to *bad.
+// to per-wave LDS counters chosen by a hash of (block, round, lane)
+// restricted to 1, 2, 16 or 256 counters, and checks that lanes hitting the
+// same counter received consecutive values in lane order. CHECK_BLOCKS
+// blocks of CHECK_THREADS run at once, several per CU on every CU, so the
+// property is checked on the LDS of every CU under load; block b writes its
+// number of violations to bad[b].
 constexpr int CHECK_THREADS = 256;
+constexpr int CHECK_BLOCKS = 1024;
+
+// Outputs of the one-time device probes below (no allocation needed): the
+// XCD of each placement-probe block, then each lane-order block's violations.
+constexpr int XCC_PROBE_BLOCKS = 256;
+__device__ uint32_t probe_out[XCC_PROBE_BLOCKS + CHECK_BLOCKS];
+
 __global__ void __launch_bounds__(CHECK_THREADS) lane_order_check_kernel(uint32_t *bad) {
+  const uint32_t salt = blockIdx.x * 0x27d4eb2fu;
   __shared__ uint32_t c[CHECK_THREADS / 64][BINS];
   __shared__ uint32_t total;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -67,7 +73,7 @@ __global__ void __launch_bounds__(CHECK_THREADS) lane_order_check_kernel(uint32_
   __syncthreads();
   uint32_t nbad = 0;
   for (uint32_t round = 0; round < 64; ++round) {
-    uint32_t h = (round * 0x9e3779b9u) ^ (tid * 0x85ebca6bu);
+    uint32_t h = (round * 0x9e3779b9u) ^ (tid * 0x85ebca6bu) ^ salt;
     h ^= h >> 15;
     h *= 0x2c1b3c6du;
     h ^= h >> 12;
@@ -90,7 +96,7 @@ __global__ void __launch_bounds__(CHECK_THREADS) lane_order_check_kernel(uint32_
   }
   if (nbad) atomicAdd(&total, nbad);
   __syncthreads();
-  if (tid == 0) *bad = total;
+  if (tid == 0) bad[blockIdx.x] = total;
 }
 
 // Where blocks land: block b records its XCD (HW_REG_XCC_ID, all 4 bits).
@@ -114,17 +120,20 @@ std::vector<CapsEntry> g_caps;
 rccl_hip_status probe_device(DeviceCaps *caps) {
   uint32_t *out = nullptr;
   hipError_t err = hipGetSymbolAddress(reinterpret_cast<void **>(&out), HIP_SYMBOL(probe_out));
-  uint32_t host[1 + XCC_PROBE_BLOCKS] = {};
+  std::vector<uint32_t> host(XCC_PROBE_BLOCKS + CHECK_BLOCKS, 0u);
   if (err == hipSuccess) {
-    lane_order_check_kernel<<<1, CHECK_THREADS>>>(out);
-    xcc_probe_kernel<<<XCC_PROBE_BLOCKS, 64>>>(out + 1);
+    xcc_probe_kernel<<<XCC_PROBE_BLOCKS, 64>>>(out);
+    lane_order_check_kernel<<<CHECK_BLOCKS, CHECK_THREADS>>>(out + XCC_PROBE_BLOCKS);
     err = hipGetLastError();
   }
-  if (err == hipSuccess) err = hipMemcpy(host, out, sizeof(host), hipMemcpyDeviceToHost);
+  if (err == hipSuccess)
+    err = hipMemcpy(host.data(), out, host.size() * sizeof(uint32_t), hipMemcpyDeviceToHost);
   if (err != hipSuccess) return set_hip_error(RCCL_HIP_ERROR_DRIVER, "radix device probe", err);
-  caps->lane_order = host[0] == 0;
+  uint64_t violations = 0;
+  for (int b = 0; b < CHECK_BLOCKS; ++b) violations += host[XCC_PROBE_BLOCKS + b];
+  caps->lane_order = violations == 0;
   bool round_robin = true;
-  for (int b = 0; b < XCC_PROBE_BLOCKS; ++b) round_robin &= host[1 + b] == uint32_t(b) % XCDS;
+  for (int b = 0; b < XCC_PROBE_BLOCKS; ++b) round_robin &= host[b] == uint32_t(b) % XCDS;
   caps->nx = round_robin ? XCDS : 1u;
   caps->rank = caps->lane_order ? Rank::LaneAtomic : Rank::MatchAny;
   int dev = 0, cus = 0;
