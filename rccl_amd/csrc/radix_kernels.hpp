@@ -215,6 +215,17 @@ histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__
                              __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   };
+  // All 8-bit digits of the key (the usual full bit range).
+  const bool all_digits = begin_bit == 0 && passes == uint32_t(PMAX) && end_bit == 8u * PMAX;
+  auto count_all = [&](Bits key) {
+    const Bits s = Ops::digit_source(key);
+#pragma unroll
+    for (int p = 0; p < PMAX; ++p) {
+      const uint32_t d = static_cast<uint32_t>(s >> (8 * p)) & 0xFFu;
+      __hip_atomic_fetch_add(&hist[(uint32_t(p) * BINS + d) * COLS + col], 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
   // With vector loads, the keys before the first 16-byte boundary and after
   // the last whole vector are counted by block 0, one per thread.
   const size_t head = VLOAD ? min<size_t>(
@@ -248,13 +259,25 @@ histogram_kernel(const Bits *__restrict__ keys, size_t n, uint32_t *__restrict__
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) k[j] = next[j];
     if (base + stride < nvec) load_chunk(base + stride);
+    if (all_digits && avail == uint32_t(CHUNK)) {
+      // Every pass of the key and a whole chunk (all but a block's last):
+      // constant digit positions, no per-key or per-pass tests.
 #pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-      if (uint32_t(j) * HIST_THREADS + tid >= avail) continue;
-      Bits kv[VEC];
-      __builtin_memcpy(kv, &k[j], sizeof(LoadT));
+      for (int j = 0; j < LOADS; ++j) {
+        Bits kv[VEC];
+        __builtin_memcpy(kv, &k[j], sizeof(LoadT));
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) count(kv[e]);
+        for (int e = 0; e < VEC; ++e) count_all(kv[e]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) {
+        if (uint32_t(j) * HIST_THREADS + tid >= avail) continue;
+        Bits kv[VEC];
+        __builtin_memcpy(kv, &k[j], sizeof(LoadT));
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) count(kv[e]);
+      }
     }
   }
   __syncthreads();
