@@ -689,8 +689,10 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     // A wave of a pass that is not skewed as a whole can still hold a skewed
     // stretch of the input (the previous pass gathers equal digits into
     // neighbouring tiles). The wave takes the skewed path when, in its first
-    // or middle item, at least RCCL_RADIX_SKEW_LANES lanes (but not all 64)
-    // share lane 0's digit.
+    // or middle item, at least RCCL_RADIX_SKEW_LANES lanes share lane 0's
+    // digit; that includes waves of presorted keys, whose items are
+    // wave-uniform (the skewed path counts such an item with one atomic), so
+    // the other path spends no test on wave-uniform items.
     auto shared_with_lane0 = [&](int j) {
       const uint32_t d =
           uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
@@ -698,7 +700,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
           __builtin_popcountll(__ballot(d == __builtin_amdgcn_readfirstlane(d))));
     };
     const uint32_t m0 = shared_with_lane0(0), m1 = shared_with_lane0(ITEMS / 2);
-    skewed = (m0 >= RCCL_RADIX_SKEW_LANES && m0 < 64) || (m1 >= RCCL_RADIX_SKEW_LANES && m1 < 64);
+    skewed = m0 >= RCCL_RADIX_SKEW_LANES || m1 >= RCCL_RADIX_SKEW_LANES;
   }
   if (skewed && lane == 0) s_skew_waves = 1;
   uint32_t *rank_slot = reinterpret_cast<uint32_t *>(stage_raw) + wave * WAVE_ITEMS + lane;
@@ -736,7 +738,8 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     for (int j = 0; j < ITEMS; ++j) {
       const uint32_t d =
           uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
-      if (wave_uniform(d)) {
+      // (With the skewed path, waves with wave-uniform items take it.)
+      if (!SKEW_PATH && wave_uniform(d)) {
         if (lane == 0)
           __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       } else {
@@ -878,7 +881,7 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
       for (int j = 0; j < ITEMS; ++j) {
         const uint32_t d =
             uint32_t(j) * 64 + lane < wave_valid ? Ops::image_digit(key[j], bit, mask) : DUMMY;
-        if (wave_uniform(d)) {
+        if (!SKEW_PATH && wave_uniform(d)) {
           uniform |= uint64_t(1) << j;
           pos[j] = lane == 0 ? __hip_atomic_fetch_add(&wcnt[d], 64u, __ATOMIC_RELAXED,
                                                       __HIP_MEMORY_SCOPE_WORKGROUP)
