@@ -925,11 +925,17 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
   // of bounds. In batches: the staged keys are read together, then their
   // digits' offsets, then stored.
   const size_t tile_base = size_t(tile) * TILE;
-  const uint32_t valid_count = static_cast<uint32_t>(min<size_t>(TILE, n - tile_base));
+  uint32_t valid_count = static_cast<uint32_t>(min<size_t>(TILE, n - tile_base));
+  // Materialized here, in a scalar register: otherwise this compiler sinks
+  // the min into the partial-tile branch below and selects on a stale scalar
+  // condition code there (valid_count came out as TILE for the last tile).
+  asm volatile("" : "+s"(valid_count));
   const uint32_t last = static_cast<uint32_t>(n - 1);
   uint32_t dst[PAIRS ? ITEMS : 1];
-#pragma unroll
-  for (int k0 = 0; k0 < ITEMS; k0 += BATCH) {
+  // One batch of keys: staged keys read together, then their digits'
+  // offsets, then stored (all items, or those before valid_count).
+  auto scatter_batch = [&](int k0, auto full) {
+    constexpr bool FULL = decltype(full)::value;
     Bits kk[BATCH];
     uint32_t off[BATCH];
 #pragma unroll
@@ -948,9 +954,23 @@ onesweep_tile(const Bits *__restrict__ keys_in, Bits *__restrict__ keys_out,
     for (int b = 0; b < BATCH && k0 + b < ITEMS; ++b) {
       const uint32_t i = uint32_t(k0 + b) * THREADS + tid;
       const uint32_t p = min(off[b] + i, last);
-      if (i < valid_count) keys_out[p] = kk[b];
+      if (FULL || i < valid_count) keys_out[p] = kk[b];
       if constexpr (PAIRS) dst[k0 + b] = p;
     }
+  };
+  if constexpr (PAIRS) {
+#pragma unroll
+    for (int k0 = 0; k0 < ITEMS; k0 += BATCH) scatter_batch(k0, std::false_type{});
+  } else if (valid_count == uint32_t(TILE)) {
+    // Every tile but the last is full: for keys only, a copy of the loop
+    // without the per-item test (and its exec-mask branch per store). (With
+    // values, the copy and the positions kept for the value stores make the
+    // 28-item shapes spill.)
+#pragma unroll
+    for (int k0 = 0; k0 < ITEMS; k0 += BATCH) scatter_batch(k0, std::true_type{});
+  } else {
+#pragma unroll
+    for (int k0 = 0; k0 < ITEMS; k0 += BATCH) scatter_batch(k0, std::false_type{});
   }
   if constexpr (PAIRS) {
     lds_barrier();
