@@ -289,17 +289,83 @@ def run_hbm_reference(torch, n, steps, warmup):
     read_ms = timed(lambda: torch.sum(words))
     ok = bool(torch.equal(dst, src)) and \
         int(torch.sum(words).item()) == (n // 2) * ((1 << 32) + 1)
-    del src, dst
+    del src, dst, words
     torch.cuda.empty_cache()
-    return {
+    out = {
         "workload": f"torch copy_ and sum of 2^{n.bit_length() - 1} u32 words on this GPU",
         "copy_ms": round(copy_ms, 4), "read_ms": round(read_ms, 4),
         "copy_GBps": round(8.0 * n / (copy_ms * 1e-3) / 1e9, 1),
         "read_GBps": round(4.0 * n / (read_ms * 1e-3) / 1e9, 1),
         "copy_frac_of_peak": round(8.0 * n / (copy_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "read_frac_of_peak": round(4.0 * n / (read_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    }
+    probe = _scatter_probe()
+    if probe is None:
+        out["scatter_probe"] = "bench_probes/libscatter_probe.so is not built"
+    else:
+        ok = ok and _time_scatter_probe(torch, probe, n, timed, out)
+    out["validated"] = ok
+    return out
+
+
+def _scatter_probe():
+    """bench_probes/libscatter_probe.so through ctypes, or None if not built."""
+    import ctypes
+
+    path = os.path.join(ROOT, "bench_probes", "libscatter_probe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.scatter_probe_tile_items.restype = ctypes.c_size_t
+    lib.scatter_probe_tile_items.argtypes = []
+    lib.scatter_probe_launch.restype = ctypes.c_int
+    lib.scatter_probe_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                         ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+def _time_scatter_probe(torch, lib, n, timed, out):
+    """The onesweep's memory pattern without its ranking (bench_probes/
+    scatter_probe.hip): a copy through LDS, the stores of a uniform radix pass
+    (256 digit runs of 68 keys per 17,408-key tile into 256 buckets), and the
+    same stores in 64-key-aligned windows, over the whole tiles of n u32 words,
+    on torch's current stream. Every output is checked exactly. Adds the rates
+    to `out`; returns whether every check held."""
+    tile = int(lib.scatter_probe_tile_items())
+    tiles = n // tile
+    m = tiles * tile
+    src = torch.arange(m, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch(mode):
+        rc = lib.scatter_probe_launch(src.data_ptr(), dst.data_ptr(), tiles, mode, stream)
+        if rc != 0:
+            raise RuntimeError(f"scatter probe mode {mode}: HIP error {rc}")
+
+    lds_copy_ms = timed(lambda: launch(0))
+    ok = bool(torch.equal(dst, src))
+    scatter_ms = timed(lambda: launch(1))
+    want = src.view(tiles, 256, tile // 256).transpose(0, 1).contiguous().view(-1)
+    ok = ok and bool(torch.equal(dst, want))
+    dst.zero_()
+    aligned_ms = timed(lambda: launch(2))
+    ok = ok and bool(torch.equal(dst, want))
+    del src, dst, want
+    torch.cuda.empty_cache()
+    moved = 8.0 * m  # bytes read + written
+    out["scatter_probe"] = {
+        "workload": f"{tiles} tiles of {tile} u32 keys, 512 threads x 34 keys, XCD runs of 8, "
+                    "two blocks per CU (bench_probes/scatter_probe.hip)",
+        "lds_copy_ms": round(lds_copy_ms, 4),
+        "lds_copy_GBps": round(moved / (lds_copy_ms * 1e-3) / 1e9, 1),
+        "scatter256_ms": round(scatter_ms, 4),
+        "scatter256_GBps": round(moved / (scatter_ms * 1e-3) / 1e9, 1),
+        "scatter256_aligned_ms": round(aligned_ms, 4),
+        "scatter256_aligned_GBps": round(moved / (aligned_ms * 1e-3) / 1e9, 1),
         "validated": ok,
     }
+    return ok
 
 
 def _median_rate(fn, items, reps=5):
@@ -874,9 +940,16 @@ def main():
                                             ref["copy_GBps"], 4)
             ref["histogram_vs_read"] = round(4.0 * n / (km["radix_histogram"] * 1e-3) / 1e9 /
                                              ref["read_GBps"], 4)
+            if isinstance(ref.get("scatter_probe"), dict):
+                ref["onesweep_vs_scatter256"] = round(
+                    8.0 * n / (km["radix_onesweep"] * 1e-3) / 1e9 /
+                    ref["scatter_probe"]["scatter256_GBps"], 4)
         out["hbm_reference"] = ref
         valid = valid and ref["validated"]
         _log(f"copy {ref['copy_GBps']} GB/s, read {ref['read_GBps']} GB/s")
+        if isinstance(ref.get("scatter_probe"), dict):
+            sp = ref["scatter_probe"]
+            _log(f"LDS copy {sp['lds_copy_GBps']} GB/s, 256-run scatter {sp['scatter256_GBps']} GB/s")
     if "pairs" in legs:
         pk, pv = wd.metric_pairs(n)
         rp = run_radix(torch, np, cub, abi, DeviceBuffer, pk, pv, args.steps, args.warmup)

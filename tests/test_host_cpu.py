@@ -47,6 +47,25 @@ def test_header_symbols_exported(lib):
     assert set(_abi.EXPORTED_SYMBOLS) <= set(names)
 
 
+def test_scatter_probe_library():
+    """bench.py's memory-pattern probe is built beside the tests, exports its
+    two entry points, and refuses bad arguments before any launch."""
+    path = os.path.join(ROOT, "bench_probes", "libscatter_probe.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert {"scatter_probe_launch", "scatter_probe_tile_items"} <= exported
+    probe = ctypes.CDLL(path)
+    probe.scatter_probe_tile_items.restype = ctypes.c_size_t
+    assert probe.scatter_probe_tile_items() == 512 * 34
+    probe.scatter_probe_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                           ctypes.c_int, ctypes.c_void_p]
+    assert probe.scatter_probe_launch(FAKE, FAKE, 1, 3, None) == 1   # no such mode
+    assert probe.scatter_probe_launch(FAKE, FAKE, 1, -1, None) == 1
+    assert probe.scatter_probe_launch(FAKE, FAKE, 0, 1, None) == 1   # no tiles
+    assert probe.scatter_probe_launch(FAKE, FAKE, 1 << 20, 0, None) == 1  # past 2^31 keys
+
+
 def test_status_strings_and_version(lib):
     assert lib.rccl_hip_abi_version() >= 1
     lib.rccl_hip_status_string.restype = ctypes.c_char_p
