@@ -20,6 +20,9 @@
 //           each lane writing the window position it owns if the run covers
 //           it. Where a run covers a whole window, its two 128-byte lines
 //           leave in one store; it takes about twice the store instructions.
+//   mode 3  mode 1 with each store split into two of 32 lanes (staged keys
+//           0-31 and 32-63 of the instruction's 64), each spanning at most
+//           two cache lines of one or two runs.
 // The input and output hold tiles * TILE u32 words (whole tiles only).
 #include <hip/hip_runtime.h>
 
@@ -85,7 +88,14 @@ probe_kernel(const uint32_t *__restrict__ in, uint32_t *__restrict__ out, uint32
       dst = base + i;
     else
       dst = size_t(i / RUN_KEYS) * bucket + size_t(tile) * RUN_KEYS + i % RUN_KEYS;
-    out[dst] = v;
+    if constexpr (MODE == 3) {
+      // Two stores of 32 lanes each (the compiler may not merge them).
+      if (lane < 32) out[dst] = v;
+      asm volatile("" ::: "memory");
+      if (lane >= 32) out[dst] = v;
+    } else {
+      out[dst] = v;
+    }
   }
 }
 
@@ -96,12 +106,12 @@ extern "C" {
 // Keys per tile: callers size the buffers to whole tiles.
 __attribute__((visibility("default"))) size_t scatter_probe_tile_items() { return TILE; }
 
-// One launch of mode 0, 1 or 2 over `tiles` whole tiles on `stream`. Returns
+// One launch of mode 0, 1, 2 or 3 over `tiles` whole tiles on `stream`. Returns
 // 0, or the HIP error of the launch; 1 for an invalid mode or tile count.
 __attribute__((visibility("default"))) int scatter_probe_launch(const void *in, void *out,
                                                                  size_t tiles, int mode,
                                                                  void *stream) {
-  if (tiles == 0 || tiles > (size_t(1) << 31) / TILE || mode < 0 || mode > 2) return 1;
+  if (tiles == 0 || tiles > (size_t(1) << 31) / TILE || mode < 0 || mode > 3) return 1;
   const size_t row = size_t(XCDS) * XCD_RUN;
   const dim3 grid(static_cast<uint32_t>((tiles + row - 1) / row * row));
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -111,8 +121,10 @@ __attribute__((visibility("default"))) int scatter_probe_launch(const void *in, 
     probe_kernel<0><<<grid, THREADS, 0, s>>>(src, dst, static_cast<uint32_t>(tiles));
   else if (mode == 1)
     probe_kernel<1><<<grid, THREADS, 0, s>>>(src, dst, static_cast<uint32_t>(tiles));
-  else
+  else if (mode == 2)
     probe_kernel<2><<<grid, THREADS, 0, s>>>(src, dst, static_cast<uint32_t>(tiles));
+  else
+    probe_kernel<3><<<grid, THREADS, 0, s>>>(src, dst, static_cast<uint32_t>(tiles));
   return static_cast<int>(hipGetLastError());
 }
 
