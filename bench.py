@@ -328,8 +328,8 @@ def _time_scatter_probe(torch, lib, n, timed, out):
     """The onesweep's memory pattern without its ranking (bench_probes/
     scatter_probe.hip): a copy through LDS, the stores of a uniform radix pass
     (256 digit runs of 68 keys per 17,408-key tile into 256 buckets), the same
-    stores in 64-key-aligned windows, and in two 32-lane halves per instruction,
-    over the whole tiles of n u32 words,
+    stores in 64-key-aligned windows, in two 32-lane halves per instruction, and
+    with tiles placed round-robin over the XCDs, over the whole tiles of n u32 words,
     on torch's current stream. Every output is checked exactly. Adds the rates
     to `out`; returns whether every check held."""
     tile = int(lib.scatter_probe_tile_items())
@@ -355,6 +355,9 @@ def _time_scatter_probe(torch, lib, n, timed, out):
     dst.zero_()
     halves_ms = timed(lambda: launch(3))
     ok = ok and bool(torch.equal(dst, want))
+    dst.zero_()
+    spread_ms = timed(lambda: launch(4))
+    ok = ok and bool(torch.equal(dst, want))
     del src, dst, want
     torch.cuda.empty_cache()
     moved = 8.0 * m  # bytes read + written
@@ -369,6 +372,8 @@ def _time_scatter_probe(torch, lib, n, timed, out):
         "scatter256_aligned_GBps": round(moved / (aligned_ms * 1e-3) / 1e9, 1),
         "scatter256_half_waves_ms": round(halves_ms, 4),
         "scatter256_half_waves_GBps": round(moved / (halves_ms * 1e-3) / 1e9, 1),
+        "scatter256_no_xcd_runs_ms": round(spread_ms, 4),
+        "scatter256_no_xcd_runs_GBps": round(moved / (spread_ms * 1e-3) / 1e9, 1),
         "validated": ok,
     }
     return ok

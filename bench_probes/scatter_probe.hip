@@ -23,6 +23,9 @@
 //   mode 3  mode 1 with each store split into two of 32 lanes (staged keys
 //           0-31 and 32-63 of the instruction's 64), each spanning at most
 //           two cache lines of one or two runs.
+//   mode 4  mode 1 with tile = block: consecutive tiles land on different
+//           XCDs (round-robin placement), so the lines two neighbouring tiles
+//           share at every run boundary meet in no common L2.
 // The input and output hold tiles * TILE u32 words (whole tiles only).
 #include <hip/hip_runtime.h>
 
@@ -52,7 +55,7 @@ template <int MODE>
 __global__ void __launch_bounds__(THREADS)
 probe_kernel(const uint32_t *__restrict__ in, uint32_t *__restrict__ out, uint32_t tiles) {
   __shared__ uint32_t stage[LDS_WORDS];
-  const uint32_t tile = xcd_order_tile(blockIdx.x);
+  const uint32_t tile = MODE == 4 ? blockIdx.x : xcd_order_tile(blockIdx.x);
   if (tile >= tiles) return;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
@@ -106,12 +109,12 @@ extern "C" {
 // Keys per tile: callers size the buffers to whole tiles.
 __attribute__((visibility("default"))) size_t scatter_probe_tile_items() { return TILE; }
 
-// One launch of mode 0, 1, 2 or 3 over `tiles` whole tiles on `stream`. Returns
+// One launch of mode 0 to 4 over `tiles` whole tiles on `stream`. Returns
 // 0, or the HIP error of the launch; 1 for an invalid mode or tile count.
 __attribute__((visibility("default"))) int scatter_probe_launch(const void *in, void *out,
                                                                  size_t tiles, int mode,
                                                                  void *stream) {
-  if (tiles == 0 || tiles > (size_t(1) << 31) / TILE || mode < 0 || mode > 3) return 1;
+  if (tiles == 0 || tiles > (size_t(1) << 31) / TILE || mode < 0 || mode > 4) return 1;
   const size_t row = size_t(XCDS) * XCD_RUN;
   const dim3 grid(static_cast<uint32_t>((tiles + row - 1) / row * row));
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -123,8 +126,10 @@ __attribute__((visibility("default"))) int scatter_probe_launch(const void *in, 
     probe_kernel<1><<<grid, THREADS, 0, s>>>(src, dst, static_cast<uint32_t>(tiles));
   else if (mode == 2)
     probe_kernel<2><<<grid, THREADS, 0, s>>>(src, dst, static_cast<uint32_t>(tiles));
-  else
+  else if (mode == 3)
     probe_kernel<3><<<grid, THREADS, 0, s>>>(src, dst, static_cast<uint32_t>(tiles));
+  else
+    probe_kernel<4><<<grid, THREADS, 0, s>>>(src, dst, static_cast<uint32_t>(tiles));
   return static_cast<int>(hipGetLastError());
 }
 

@@ -60,7 +60,7 @@ def test_scatter_probe_library():
     assert probe.scatter_probe_tile_items() == 512 * 34
     probe.scatter_probe_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
                                            ctypes.c_int, ctypes.c_void_p]
-    assert probe.scatter_probe_launch(FAKE, FAKE, 1, 4, None) == 1   # no such mode
+    assert probe.scatter_probe_launch(FAKE, FAKE, 1, 5, None) == 1   # no such mode
     assert probe.scatter_probe_launch(FAKE, FAKE, 1, -1, None) == 1
     assert probe.scatter_probe_launch(FAKE, FAKE, 0, 1, None) == 1   # no tiles
     assert probe.scatter_probe_launch(FAKE, FAKE, 1 << 20, 0, None) == 1  # past 2^31 keys
